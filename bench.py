@@ -1,0 +1,185 @@
+#!/usr/bin/env python3
+"""Benchmark of the unmasking generator on one MI355X.
+
+Metric: utterance RTF + unmask steps/s for a 10 s utterance (250 frames at
+25 fps, 80 text tokens), 32 steps, CFG 2.0, on the 28-layer Qwen3-0.6B-shaped
+backbone with seeded random fp16 weights (synthetic; no checkpoint) and
+seeded Gumbel position noise at temperature 5.0.
+
+A benchmark "step" is one whole utterance: Generator::Generate, i.e. 32
+unmasking steps (forward of the packed CFG batch, CFG scoring, top-k
+selection) with the inputs already resident on the device and only the
+final codes copied back. `value` is unmask steps per second
+(32 x utterances / wall time); `utterance_rtf` is wall time per utterance
+over 10 s.
+
+Also reported: the roofline of the dominant kernel (algorithmic FLOPs or
+bytes per launch over its HIP-event-timed launch duration on the library
+stream) and the CPU baseline (the oracle's float32 restatement of the
+reference's path, one unmasking step of the same workload on the host).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (text tokens, reference frames, target frames)
+    "10s": (80, 0, 250),
+    "2s": (20, 0, 50),
+    "clone": (180, 125, 375),
+}
+
+
+def make_input(ov, text, reference, target, seed=42):
+    rng = np.random.default_rng(seed)
+    tokens = rng.integers(0, 151936, size=text)
+    refc = rng.integers(0, 1024, size=(8, reference)) if reference else None
+    return ov.ConditionalInput.build(tokens, refc, reference, target)
+
+
+def cpu_baseline(cfg, x, decoding, steps):
+    """The oracle (float32, all host threads up to 16) timed on `steps`
+    unmasking steps of the workload: forward, score and select."""
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    oracle.lib().orc_set_threads(threads)
+    t0 = time.perf_counter()
+    model = oracle.Model(cfg, 1234)
+    setup = time.perf_counter() - t0
+    ids = np.ascontiguousarray(x.ids)
+    C, F, V = 8, x.target_frames, 1025
+    sel = oracle.Selector(decoding.layer_penalty, decoding.position_temperature, 42)
+    codes = np.full(C * F, 1024, dtype=np.int32)
+    schedule = oracle.unmask_schedule(C * F, 32, decoding.t_shift)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        logits = model.forward(ids, x.audio_start, F)
+        pred, conf = oracle.score(logits, F, C, V, 1024, decoding.guidance)
+        sel.fill(schedule[s], C, F, pred, conf, 1024, codes)
+    elapsed = time.perf_counter() - t0
+    return {"value": steps / elapsed, "unit": "unmask steps/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{steps} unmasking step(s) of the {F}-frame workload "
+                      f"(forward of {x.length + F} packed rows, score, select), "
+                      f"float32 oracle; weight synthesis {setup:.1f} s excluded",
+            "utterance_rtf_extrapolated": (elapsed / steps * 32) / (F / 25.0)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="10s", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-steps", type=int, default=2,
+                    help="unmasking steps timed for the CPU baseline (0 skips it)")
+    ap.add_argument("--profile-repeats", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is design-only)"}))
+        sys.exit(2)
+
+    import torch
+    import omnivoice_amd as ov
+    if not torch.cuda.is_available():
+        raise SystemExit("no GPU visible")
+
+    cfg = ov.released_config()
+    text, reference, target = WORKLOADS[args.workload]
+    x = make_input(ov, text, reference, target)
+    decoding = ov.DecodingConfig(steps=32, guidance=2.0, t_shift=0.1,
+                                 layer_penalty=5.0, position_temperature=5.0)
+    t0 = time.perf_counter()
+    gen = ov.Generator.synthetic(cfg, 1234)
+    load_s = time.perf_counter() - t0
+    executed = sum(1 for c in ov.unmask_schedule(8 * target, 32, 0.1) if c)
+
+    for i in range(args.warmup):
+        gen.generate(x, decoding, seed=42 + i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        gen.generate(x, decoding, seed=42 + i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_utterance = elapsed / args.steps * 1e3
+    steps_per_s = executed * args.steps / elapsed
+    rtf = (elapsed / args.steps) / (target / 25.0)
+
+    stats = gen.profile(x, repeats=args.profile_repeats)
+    kernels = {}
+    for name, s in stats.items():
+        avg = s["total_ms"] / s["launches"]
+        kernels[name] = {"launches": s["launches"], "avg_us": avg * 1e3,
+                         "share": 0.0,
+                         "tflops": s["flops"] / (s["total_ms"] * 1e-3) / 1e12
+                         if s["flops"] else None,
+                         "gbs": s["bytes"] / (s["total_ms"] * 1e-3) / 1e9}
+    total_ms = sum(s["total_ms"] for s in stats.values())
+    for name, s in stats.items():
+        kernels[name]["share"] = s["total_ms"] / total_ms
+    dominant = max(stats, key=lambda n: stats[n]["total_ms"])
+    d = stats[dominant]
+    per_launch_ms = d["total_ms"] / d["launches"]
+    if d["flops"]:
+        achieved = d["flops"] / d["launches"] / (per_launch_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": achieved / PEAK_FP16_TFLOPS,
+                    "traffic": None, "kernel": dominant,
+                    "avg_launch_us": per_launch_ms * 1e3}
+    else:
+        achieved = d["bytes"] / d["launches"] / (per_launch_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+                    "traffic": None, "kernel": dominant,
+                    "avg_launch_us": per_launch_ms * 1e3}
+    gemm_ms = sum(s["total_ms"] for n, s in stats.items() if n.startswith("gemm_")
+                  and n != "gemm_audio_heads")
+    gemm_flops = sum(s["flops"] for n, s in stats.items() if n.startswith("gemm_")
+                     and n != "gemm_audio_heads")
+
+    result = {
+        "metric": "utterance RTF + unmask steps/s, 10 s speech, 32 steps, CFG 2.0, 1 GPU",
+        "value": steps_per_s,
+        "unit": "unmask steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_utterance,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0, 0.02) fp16 weights, uniform text ids, masked target)",
+        "config": {"workload": f"{args.workload}: {text} text tokens, {reference} "
+                               f"reference frames, {target} masked target frames, "
+                               f"CFG pair packed as {text + reference + 2 * target} rows, "
+                               f"32 steps, guidance 2.0, position temperature 5.0",
+                   "backbone": "28 x Qwen3 (hidden 1024, 16q/8kv x 128, FFN 3072)",
+                   "parallelism": "single GPU"},
+        "utterance_rtf": rtf,
+        "unmask_steps_per_utterance": executed,
+        "roofline": roofline,
+        "backbone_gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
+        "eager_step_ms": total_ms / args.profile_repeats,
+        "kernels": kernels,
+        "load_s": load_s,
+    }
+    if args.cpu_steps > 0:
+        result["cpu_baseline"] = cpu_baseline(cfg, x, decoding, args.cpu_steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,179 @@
+// Launchers of the gfx950 generator kernels. Every launcher validates the
+// shapes its kernel assumes and throws ovg::Error instead of launching on a
+// shape the kernel cannot cover.
+#ifndef OMNIVOICE_AMD_KERNELS_HPP_
+#define OMNIVOICE_AMD_KERNELS_HPP_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "common.hpp"
+
+namespace ovg {
+
+class Error : public std::runtime_error {
+ public:
+  using std::runtime_error::runtime_error;
+};
+
+inline void Check(hipError_t status, const char* what) {
+  if (status != hipSuccess)
+    throw Error(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+inline void Require(bool condition, const std::string& what) {
+  if (!condition)
+    throw Error(what);
+}
+
+// ---------------------------------------------------------------- GEMM
+// Y = X W^T: X fp16 [M][K] (row stride lda), W fp16 [N][K] (ldb), fp32
+// accumulation; the epilogue decides what is written.
+enum class Epilogue : int {
+  kStore = 0,       // y fp32 [M][ldc] = acc
+  kAccumulate = 1,  // y fp32 [M][ldc] += acc (the residual stream)
+  kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
+                    // qk [M][ldq]; v heads -> fp16 V^T vt[g][d][ldvt]
+  kSwiGlu = 3,      // W rows interleaved per 128-row tile as 64 gate rows
+                    // then the matching 64 up rows; act fp16 [M][ldh] =
+                    // silu(gate) * up
+};
+
+struct GemmParams {
+  const half_t* x;
+  const half_t* w;
+  int lda, ldb;
+  int m, n, k;
+  int splits;        // K split into `splits` equal ranges (1 = none)
+  float* partials;   // [tiles * splits][tile floats] when splits > 1
+  int* counters;     // [tiles], zero between launches
+  // kStore / kAccumulate
+  float* y;
+  int ldc;
+  // kQkvRope
+  half_t* qk;
+  int ldq;
+  half_t* vt;
+  int ldvt;
+  const float* q_norm;
+  const float* k_norm;
+  const float2* rope;      // [position][head_dim / 2] (cos, sin)
+  const int* positions;    // [M]
+  int heads, kv_heads;
+  float eps;
+  // kSwiGlu
+  half_t* act;
+  int ldh;
+};
+
+// Picks the tile shape and split count for (m, n, k); returns the number
+// of floats of `partials` and ints of `counters` the launch needs.
+struct GemmPlan {
+  int block_m = 128;
+  int splits = 1;
+  int tiles = 0;
+  std::size_t partial_floats = 0;
+};
+GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue);
+void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
+                hipStream_t stream);
+
+// ---------------------------------------------------------------- rows
+struct EmbedParams {
+  const int* ids;          // [codebooks][ld_ids]
+  int ld_ids;
+  const int* row_kind;     // [rows]: 0 text, 1 audio, 2 padding
+  const float* text;       // [vocab][hidden]
+  const float* audio;      // [codebooks * vocab][hidden]
+  const float* norm;       // first layer's input norm [hidden]
+  float* hidden;           // [rows][hidden]
+  half_t* normed;          // [rows][hidden]
+  int rows, hidden_size, codebooks, vocab;
+  float eps;
+  int* epoch;              // incremented once per launch (may be null)
+};
+void LaunchEmbed(const EmbedParams& p, hipStream_t stream);
+
+// normed[r] = half(w * x[r] * rsqrt(mean(x[r]^2) + eps)), r < rows; with
+// `gather` non-null the source row is gather[r].
+void LaunchRmsNorm(const float* x, const int* gather, const float* w,
+                   half_t* out, int rows, int width, float eps,
+                   hipStream_t stream);
+
+// vt[g][d][ldvt] = qkv[r][(heads + kv_heads + g) * 128 + d] for r < rows.
+void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
+                      int rows, int heads, int kv_heads, hipStream_t stream);
+
+void LaunchFill(int* data, int value, int count, hipStream_t stream);
+
+// ---------------------------------------------------------------- attention
+struct AttentionWork {
+  int q_begin, q_count, seq_begin, seq_length;
+};
+struct AttentionParams {
+  const half_t* qk;        // [rows][ld_qk]: q heads, then k heads
+  const half_t* vt;        // [kv_heads][128][ldvt]
+  half_t* out;             // [rows][heads * 128]
+  const AttentionWork* work;
+  int work_count;
+  int ld_qk, ldvt, heads, kv_heads;
+  float scale_log2;        // log2(e) / sqrt(128)
+};
+void LaunchAttention(const AttentionParams& p, hipStream_t stream);
+
+// ---------------------------------------------------------------- decoding
+// Per item: logits rows [logit_row, logit_row + frames) conditional,
+// [logit_row + frames, logit_row + 2 frames) unconditional; outputs
+// [codebook][frame] at out_base.
+struct ScoreItem {
+  int logit_row, frames, out_base, pad;
+};
+struct ScoreParams {
+  const float* logits;
+  const ScoreItem* items;
+  int item_count, max_frames;
+  int codebooks, vocab, width;
+  unsigned mask_id;
+  float guidance;
+  int* prediction;
+  float* confidence;
+};
+void LaunchScore(const ScoreParams& p, hipStream_t stream);
+
+// One work-group per item. The step's (step, count, noise offset) come from
+// `plan[(epoch - 1) * items + item]` when `epoch` is non-null, else from
+// the by-value fields.
+struct SelectItem {
+  int frames, out_base;      // pred/conf/codes/unmasked_at offset
+  int cond_row, uncond_row;  // first packed row of the target frames
+};
+struct SelectStep {
+  int step, count, noise_offset, pad;
+};
+struct SelectParams {
+  const int* prediction;
+  const float* confidence;
+  const float* noise;
+  int* codes;
+  int* unmasked_at;
+  int* ids;                  // packed [codebooks][ld_ids] or null
+  int ld_ids;
+  const SelectItem* items;
+  int item_count;
+  int codebooks;
+  float layer_penalty, temperature;
+  unsigned mask_id;
+  const SelectStep* plan;
+  const int* epoch;
+  SelectStep single;
+};
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectPerThread = 16;
+void LaunchSelect(const SelectParams& p, int max_total, hipStream_t stream);
+
+}  // namespace ovg
+
+#endif  // OMNIVOICE_AMD_KERNELS_HPP_

@@ -1,0 +1,245 @@
+// Device operators on caller-owned device pointers (include/omnivoice_mi355x.h,
+// "Device operators"): each is one launcher of the generator's kernels
+// behind the C ABI, for integration and for per-kernel parity tests.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "../../include/omnivoice_mi355x.h"
+#include "kernels.hpp"
+
+namespace {
+
+void SetError(char* error, std::size_t len, const std::string& message) {
+  if (error == nullptr || len == 0)
+    return;
+  const std::size_t n = std::min(len - 1, message.size());
+  std::memcpy(error, message.data(), n);
+  error[n] = '\0';
+}
+
+template <typename F>
+int Guard(const char* prefix, char* error, std::size_t len, F&& body) {
+  try {
+    body();
+    return OVG_OK;
+  } catch (const std::exception& failure) {
+    SetError(error, len, std::string(prefix) + failure.what());
+    return OVG_ERROR;
+  }
+}
+
+bool FitsInt(int64_t v) { return v >= 0 && v <= (int64_t{1} << 30); }
+
+// A device allocation that lives for one operator call.
+template <typename T>
+struct Scratch {
+  T* data = nullptr;
+  explicit Scratch(std::size_t count) {
+    ovg::Check(hipMalloc(reinterpret_cast<void**>(&data),
+                         std::max<std::size_t>(count, 1) * sizeof(T)),
+               "hipMalloc");
+  }
+  ~Scratch() {
+    if (data != nullptr)
+      (void)hipFree(data);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int ovg_op_score(const float* logits, int32_t* prediction, float* confidence,
+                 int64_t frames, int64_t codebooks, int64_t vocab,
+                 uint32_t mask_id, float guidance, void* stream, char* error,
+                 size_t error_len) {
+  return Guard("score: ", error, error_len, [&] {
+    ovg::Require(logits && prediction && confidence, "null pointer");
+    ovg::Require(frames >= 1 && FitsInt(frames) && codebooks >= 1 &&
+                     codebooks <= 64 && vocab >= 1 && vocab <= 1088,
+                 "shape outside the kernel's range");
+    auto s = static_cast<hipStream_t>(stream);
+    Scratch<ovg::ScoreItem> item(1);
+    const ovg::ScoreItem host{0, static_cast<int>(frames), 0, 0};
+    ovg::Check(hipMemcpyAsync(item.data, &host, sizeof(host),
+                              hipMemcpyHostToDevice, s),
+               "upload");
+    ovg::ScoreParams p{};
+    p.logits = logits;
+    p.items = item.data;
+    p.item_count = 1;
+    p.max_frames = static_cast<int>(frames);
+    p.codebooks = static_cast<int>(codebooks);
+    p.vocab = static_cast<int>(vocab);
+    p.width = p.codebooks * p.vocab;
+    p.mask_id = mask_id;
+    p.guidance = guidance;
+    p.prediction = prediction;
+    p.confidence = confidence;
+    ovg::LaunchScore(p, s);
+    ovg::Check(hipStreamSynchronize(s), "score");
+  });
+}
+
+int ovg_op_select(const int32_t* prediction, const float* confidence,
+                  const float* noise, int32_t* codes, int32_t* unmasked_at,
+                  int64_t codebooks, int64_t frames, int64_t count,
+                  int32_t step, float layer_penalty, float temperature,
+                  uint32_t mask_id, void* stream, char* error,
+                  size_t error_len) {
+  return Guard("select: ", error, error_len, [&] {
+    ovg::Require(prediction && confidence && codes && unmasked_at,
+                 "null pointer");
+    ovg::Require(temperature <= 0.0F || noise != nullptr,
+                 "noise required when the temperature is positive");
+    ovg::Require(codebooks >= 1 && frames >= 1 &&
+                     codebooks * frames <=
+                         ovg::kSelectThreads * ovg::kSelectPerThread,
+                 "codebooks * frames outside [1, 16384]");
+    ovg::Require(count >= 0, "negative count");
+    auto s = static_cast<hipStream_t>(stream);
+    Scratch<ovg::SelectItem> item(1);
+    const ovg::SelectItem host{static_cast<int>(frames), 0, 0, 0};
+    ovg::Check(hipMemcpyAsync(item.data, &host, sizeof(host),
+                              hipMemcpyHostToDevice, s),
+               "upload");
+    ovg::SelectParams p{};
+    p.prediction = prediction;
+    p.confidence = confidence;
+    p.noise = noise;
+    p.codes = codes;
+    p.unmasked_at = unmasked_at;
+    p.ids = nullptr;
+    p.items = item.data;
+    p.item_count = 1;
+    p.codebooks = static_cast<int>(codebooks);
+    p.layer_penalty = layer_penalty;
+    p.temperature = temperature;
+    p.mask_id = mask_id;
+    p.plan = nullptr;
+    p.epoch = nullptr;
+    p.single = {step, static_cast<int>(std::min<int64_t>(count, 1 << 30)), 0, 0};
+    ovg::LaunchSelect(p, static_cast<int>(codebooks * frames), s);
+    ovg::Check(hipStreamSynchronize(s), "select");
+  });
+}
+
+int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
+                  int64_t in, int64_t out, int accumulate, void* stream,
+                  char* error, size_t error_len) {
+  return Guard("linear: ", error, error_len, [&] {
+    ovg::Require(x && w && y, "null pointer");
+    ovg::Require(rows >= 1 && in >= 64 && out >= 1 && FitsInt(rows) &&
+                     FitsInt(in) && FitsInt(out),
+                 "empty or oversized shape");
+    auto s = static_cast<hipStream_t>(stream);
+    const auto epi =
+        accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;
+    const ovg::GemmPlan plan = ovg::PlanGemm(
+        static_cast<int>(rows), static_cast<int>(out), static_cast<int>(in), epi);
+    Scratch<float> partials(plan.partial_floats);
+    Scratch<int> counters(static_cast<std::size_t>(plan.tiles));
+    ovg::Check(hipMemsetAsync(counters.data, 0,
+                              static_cast<std::size_t>(plan.tiles) * sizeof(int), s),
+               "clear counters");
+    ovg::GemmParams p{};
+    p.x = static_cast<const ovg::half_t*>(x);
+    p.w = static_cast<const ovg::half_t*>(w);
+    p.lda = static_cast<int>(in);
+    p.ldb = static_cast<int>(in);
+    p.m = static_cast<int>(rows);
+    p.n = static_cast<int>(out);
+    p.k = static_cast<int>(in);
+    p.splits = plan.splits;
+    p.partials = partials.data;
+    p.counters = counters.data;
+    p.y = y;
+    p.ldc = static_cast<int>(out);
+    ovg::LaunchGemm(p, plan, epi, s);
+    ovg::Check(hipStreamSynchronize(s), "linear");
+  });
+}
+
+int ovg_op_rmsnorm(const float* input, const float* weight, void* output,
+                   int64_t rows, int64_t width, float epsilon, void* stream,
+                   char* error, size_t error_len) {
+  return Guard("rmsnorm: ", error, error_len, [&] {
+    ovg::Require(input && weight && output, "null pointer");
+    ovg::Require(rows >= 1 && FitsInt(rows), "bad rows");
+    auto s = static_cast<hipStream_t>(stream);
+    ovg::LaunchRmsNorm(input, nullptr, weight,
+                       static_cast<ovg::half_t*>(output), static_cast<int>(rows),
+                       static_cast<int>(width), epsilon, s);
+    ovg::Check(hipStreamSynchronize(s), "rmsnorm");
+  });
+}
+
+int ovg_op_attention(const void* qkv, void* output, int64_t rows,
+                     int64_t heads, int64_t kv_heads,
+                     const int64_t* sequences, int64_t count, void* stream,
+                     char* error, size_t error_len) {
+  return Guard("attention: ", error, error_len, [&] {
+    ovg::Require(qkv && output && sequences, "null pointer");
+    ovg::Require(rows >= 1 && FitsInt(rows) && heads >= 1 && kv_heads >= 1 &&
+                     heads <= 64 && count >= 1,
+                 "bad shape");
+    const int ld_qkv = static_cast<int>((heads + 2 * kv_heads) * 128);
+    std::vector<ovg::AttentionWork> work;
+    int64_t end = 0;
+    for (int64_t i = 0; i < count; ++i) {
+      const int64_t first = sequences[2 * i], length = sequences[2 * i + 1];
+      ovg::Require(first >= 0 && length >= 1 && first + length <= rows,
+                   "sequence outside the rows");
+      ovg::Require(first % ovg::kSequenceAlign == 0,
+                   "sequence start must be a multiple of 8");
+      end = std::max(end, first + (length + 31) / 32 * 32);
+      for (int64_t q = 0; q < length; q += 32)
+        work.push_back({static_cast<int>(first + q),
+                        static_cast<int>(std::min<int64_t>(32, length - q)),
+                        static_cast<int>(first), static_cast<int>(length)});
+    }
+    auto s = static_cast<hipStream_t>(stream);
+    // Keys are read in whole 32-row tiles: copy q|k into a buffer padded to
+    // the last tile, and V into V^T.
+    const int padded = static_cast<int>(std::max(end, rows));
+    const int ldvt = (padded + 7) / 8 * 8;
+    Scratch<ovg::half_t> qk(static_cast<std::size_t>(padded) * ld_qkv);
+    Scratch<ovg::half_t> vt(static_cast<std::size_t>(kv_heads) * 128 * ldvt);
+    Scratch<ovg::AttentionWork> dwork(work.size());
+    ovg::Check(hipMemsetAsync(qk.data, 0,
+                              static_cast<std::size_t>(padded) * ld_qkv * 2, s),
+               "clear");
+    ovg::Check(hipMemsetAsync(vt.data, 0,
+                              static_cast<std::size_t>(kv_heads) * 128 * ldvt * 2, s),
+               "clear");
+    ovg::Check(hipMemcpyAsync(qk.data, qkv,
+                              static_cast<std::size_t>(rows) * ld_qkv * 2,
+                              hipMemcpyDeviceToDevice, s),
+               "copy");
+    ovg::Check(hipMemcpyAsync(dwork.data, work.data(),
+                              work.size() * sizeof(ovg::AttentionWork),
+                              hipMemcpyHostToDevice, s),
+               "upload");
+    ovg::LaunchTransposeV(static_cast<const ovg::half_t*>(qkv), ld_qkv,
+                          vt.data, ldvt, static_cast<int>(rows),
+                          static_cast<int>(heads), static_cast<int>(kv_heads), s);
+    ovg::AttentionParams p{};
+    p.qk = qk.data;
+    p.vt = vt.data;
+    p.out = static_cast<ovg::half_t*>(output);
+    p.work = dwork.data;
+    p.work_count = static_cast<int>(work.size());
+    p.ld_qk = ld_qkv;
+    p.ldvt = ldvt;
+    p.heads = static_cast<int>(heads);
+    p.kv_heads = static_cast<int>(kv_heads);
+    p.scale_log2 = 1.44269504088896341F / 11.313708498984761F;
+    ovg::LaunchAttention(p, s);
+    ovg::Check(hipStreamSynchronize(s), "attention");
+  });
+}
+
+}  // extern "C"

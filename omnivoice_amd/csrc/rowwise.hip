@@ -1,0 +1,176 @@
+// Row-wise kernels of the generator: the embedding gather-sum fused with the
+// first layer's input RMSNorm, RMSNorm (optionally gathering rows), the V
+// transpose used by the attention operator, and an int fill (used instead of
+// hipMemsetAsync so that captured graphs hold kernel nodes only).
+//
+// One 256-thread work-group per row; each thread owns float4 columns, so a
+// 1024-wide row is one float4 per thread and the sum of squares is a wave
+// butterfly plus a fixed-order sum of the four wave totals.
+#include "kernels.hpp"
+
+namespace ovg {
+namespace {
+
+constexpr int kRowThreads = 256;
+
+__device__ __forceinline__ float BlockSum(float v, float* scratch) {
+  v = WaveSum(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0)
+    scratch[wave] = v;
+  __syncthreads();
+  const float total = (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+  __syncthreads();
+  return total;
+}
+
+// kernels::Embed (reference kernels/generator_kernels.hip:62-83): text rows
+// copy their token's float32 row, audio rows sum the 8 codebooks'
+// embeddings of their codes (a masked frame sums the 8 mask rows),
+// padding rows are zero. Then RMSNorm with the first layer's input norm
+// (kernels/generator_kernels.hip:85-97).
+__global__ __launch_bounds__(kRowThreads) void EmbedKernel(EmbedParams p) {
+  __shared__ float scratch[4];
+  const int row = blockIdx.x;
+  if (p.epoch != nullptr && row == 0 && threadIdx.x == 0)
+    *p.epoch += 1;
+  const int kind = p.row_kind[row];
+  float* out = p.hidden + static_cast<size_t>(row) * p.hidden_size;
+  half_t* normed = p.normed + static_cast<size_t>(row) * p.hidden_size;
+  float squares = 0.0F;
+  constexpr int kMaxChunks = 4;  // hidden <= 4096
+  floatx4 v[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int d = (threadIdx.x + i * kRowThreads) * 4;
+    v[i] = floatx4{0, 0, 0, 0};
+    if (d >= p.hidden_size)
+      continue;
+    if (kind == 0) {
+      const int id = p.ids[row];
+      v[i] = *reinterpret_cast<const floatx4*>(
+          p.text + static_cast<size_t>(id) * p.hidden_size + d);
+    } else if (kind == 1) {
+      for (int c = 0; c < p.codebooks; ++c) {
+        const size_t entry = static_cast<size_t>(c) * p.vocab +
+                             p.ids[static_cast<size_t>(c) * p.ld_ids + row];
+        v[i] += *reinterpret_cast<const floatx4*>(
+            p.audio + entry * p.hidden_size + d);
+      }
+    }
+    *reinterpret_cast<floatx4*>(out + d) = v[i];
+    squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
+               v[i][3] * v[i][3];
+  }
+  const float total = BlockSum(squares, scratch);
+  const float scale =
+      rsqrtf(total / static_cast<float>(p.hidden_size) + p.eps);
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int d = (threadIdx.x + i * kRowThreads) * 4;
+    if (d >= p.hidden_size)
+      continue;
+    const floatx4 w = *reinterpret_cast<const floatx4*>(p.norm + d);
+    const half4 h = {static_cast<half_t>(w[0] * (v[i][0] * scale)),
+                     static_cast<half_t>(w[1] * (v[i][1] * scale)),
+                     static_cast<half_t>(w[2] * (v[i][2] * scale)),
+                     static_cast<half_t>(w[3] * (v[i][3] * scale))};
+    *reinterpret_cast<half4*>(normed + d) = h;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void RmsNormKernel(
+    const float* x, const int* gather, const float* w, half_t* out, int width,
+    float eps) {
+  __shared__ float scratch[4];
+  const int row = blockIdx.x;
+  const int src = gather != nullptr ? gather[row] : row;
+  const float* in = x + static_cast<size_t>(src) * width;
+  constexpr int kMaxChunks = 4;
+  floatx4 v[kMaxChunks];
+  float squares = 0.0F;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int d = (threadIdx.x + i * kRowThreads) * 4;
+    v[i] = floatx4{0, 0, 0, 0};
+    if (d < width) {
+      v[i] = *reinterpret_cast<const floatx4*>(in + d);
+      squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
+                 v[i][3] * v[i][3];
+    }
+  }
+  const float total = BlockSum(squares, scratch);
+  const float scale = rsqrtf(total / static_cast<float>(width) + eps);
+  half_t* o = out + static_cast<size_t>(row) * width;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int d = (threadIdx.x + i * kRowThreads) * 4;
+    if (d >= width)
+      continue;
+    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + d);
+    const half4 h = {static_cast<half_t>(wv[0] * (v[i][0] * scale)),
+                     static_cast<half_t>(wv[1] * (v[i][1] * scale)),
+                     static_cast<half_t>(wv[2] * (v[i][2] * scale)),
+                     static_cast<half_t>(wv[3] * (v[i][3] * scale))};
+    *reinterpret_cast<half4*>(o + d) = h;
+  }
+}
+
+// One thread per (kv head, dim, row).
+__global__ void TransposeVKernel(const half_t* qkv, int ld_qkv, half_t* vt,
+                                 int ldvt, int rows, int heads, int kv_heads) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  const int d = blockIdx.y;
+  const int g = blockIdx.z;
+  if (row >= rows)
+    return;
+  vt[static_cast<size_t>(g * 128 + d) * ldvt + row] =
+      qkv[static_cast<size_t>(row) * ld_qkv + (heads + kv_heads + g) * 128 + d];
+}
+
+__global__ void FillKernel(int* data, int value, int count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count)
+    data[i] = value;
+}
+
+}  // namespace
+
+void LaunchEmbed(const EmbedParams& p, hipStream_t stream) {
+  Require(p.rows > 0, "embed: no rows");
+  Require(p.hidden_size % 4 == 0 && p.hidden_size <= 4 * 4 * kRowThreads,
+          "embed: hidden size must be a multiple of 4 and at most 4096");
+  hipLaunchKernelGGL(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream,
+                     p);
+  Check(hipGetLastError(), "embed launch");
+}
+
+void LaunchRmsNorm(const float* x, const int* gather, const float* w,
+                   half_t* out, int rows, int width, float eps,
+                   hipStream_t stream) {
+  Require(rows > 0, "rmsnorm: no rows");
+  Require(width % 4 == 0 && width <= 4 * 4 * kRowThreads,
+          "rmsnorm: width must be a multiple of 4 and at most 4096");
+  hipLaunchKernelGGL(RmsNormKernel, dim3(rows), dim3(kRowThreads), 0, stream,
+                     x, gather, w, out, width, eps);
+  Check(hipGetLastError(), "rmsnorm launch");
+}
+
+void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
+                      int rows, int heads, int kv_heads, hipStream_t stream) {
+  Require(rows > 0 && ldvt >= rows, "transpose: bad rows");
+  const dim3 grid((rows + 255) / 256, 128, kv_heads);
+  hipLaunchKernelGGL(TransposeVKernel, grid, dim3(256), 0, stream, qkv,
+                     ld_qkv, vt, ldvt, rows, heads, kv_heads);
+  Check(hipGetLastError(), "transpose launch");
+}
+
+void LaunchFill(int* data, int value, int count, hipStream_t stream) {
+  if (count <= 0)
+    return;
+  hipLaunchKernelGGL(FillKernel, dim3((count + 255) / 256), dim3(256), 0,
+                     stream, data, value, count);
+  Check(hipGetLastError(), "fill launch");
+}
+
+}  // namespace ovg

@@ -1,0 +1,269 @@
+"""ORACLE — test infrastructure, not product code.
+
+ctypes bindings of the CPU restatement (liboracle.so, built by
+oracle/Makefile) and of the reference's own decoding.cpp compiled into
+oracle/_ref/. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import this package, as the checker or as the timed CPU
+baseline; the product package never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libref_decoding.so")
+
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+_ptr = ctypes.c_void_p
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [("vocab_size", _i64), ("hidden_size", _i64),
+                ("intermediate_size", _i64), ("layers", _i64),
+                ("heads", _i64), ("kv_heads", _i64), ("head_dim", _i64),
+                ("max_positions", _i64), ("rms_norm_eps", _f32),
+                ("rope_theta", _f32), ("audio_codebooks", _i64),
+                ("audio_vocab_size", _i64), ("audio_mask_id", _u32)]
+
+
+def build(reference: bool = True) -> None:
+    """Compiles liboracle.so and, when the reference tree is present,
+    _ref/libref_decoding.so."""
+    subprocess.run(["make", "-B", "-C", HERE, "-j8", "all"], check=True,
+                   stdout=subprocess.DEVNULL)
+    if reference and os.path.isdir("/root/reference"):
+        subprocess.run(["make", "-B", "-C", HERE, "ref"], check=True,
+                       stdout=subprocess.DEVNULL)
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built (run make -C oracle)")
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "orc_unmask_schedule": (None, [_i64, _i64, _f32, _ptr]),
+        "orc_build_input": (_i64, [_ptr, _i64, _ptr, _i64, _i64, _i64, _u32, _ptr]),
+        "orc_exp": (_f32, [_f32]),
+        "orc_log": (_f32, [_f32]),
+        "orc_score": (None, [_ptr, _i64, _i64, _i64, _u32, _f32, _ptr, _ptr]),
+        "orc_selector_create": (_ptr, [_f32, _f32, _u64]),
+        "orc_selector_destroy": (None, [_ptr]),
+        "orc_selector_fill": (_i64, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _u32, _ptr, _ptr]),
+        "orc_selector_noise": (None, [_ptr, _i64, _ptr]),
+        "orc_mt19937_64_nth": (_u64, [_u64, _i64]),
+        "orc_generate_from_logits": (_i64, [_ptr, _i64, _i64, _i64, _i64, _u32, _i64,
+                                            _f32, _f32, _f32, _f32, _u64, _ptr, _ptr]),
+        "orc_synth_normal": (ctypes.c_double, [_u64, _u64, _u64]),
+        "orc_round_half": (_f32, [_f32]),
+        "orc_synth_values": (None, [_u64, _u64, _u64, _i64, ctypes.c_int, _f32, _ptr]),
+        "orc_model_synthetic": (_ptr, [ctypes.POINTER(OrcConfig), _u64, _f32]),
+        "orc_model_from_host": (_ptr, [ctypes.POINTER(OrcConfig), _ptr, _ptr, _ptr, _ptr, _ptr]),
+        "orc_model_destroy": (None, [_ptr]),
+        "orc_set_threads": (None, [ctypes.c_int]),
+        "orc_forward": (None, [_ptr, _ptr, _i64, _i64, _i64, ctypes.c_int, _ptr]),
+        "orc_generate": (None, [_ptr, _ptr, _i64, _i64, _i64, ctypes.c_int, _i64, _f32,
+                                _f32, _f32, _f32, _u64, _ptr, _ptr]),
+        "orc_rmsnorm": (None, [_ptr, _ptr, _ptr, _i64, _i64, _f32]),
+        "orc_linear": (None, [_ptr, _ptr, _ptr, _i64, _i64, _i64, ctypes.c_int]),
+        "orc_qk_norm_rope": (None, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
+                                    _f32, _f32]),
+        "orc_attention": (None, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, ctypes.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+_ref: Optional[ctypes.CDLL] = None
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref() -> ctypes.CDLL:
+    """The reference's decoding.cpp (oracle/_ref)."""
+    global _ref
+    if _ref is not None:
+        return _ref
+    R = ctypes.CDLL(REF_PATH)
+    R.ref_unmask_schedule.argtypes = [_i64, _i64, _f32, _ptr]
+    R.ref_unmask_schedule.restype = None
+    R.ref_build_input.argtypes = [_ptr, _i64, _ptr, _i64, _i64, _i64, _u32, _ptr]
+    R.ref_build_input.restype = _i64
+    R.ref_selector_create.argtypes = [_f32, _f32, _u64]
+    R.ref_selector_create.restype = _ptr
+    R.ref_selector_destroy.argtypes = [_ptr]
+    R.ref_selector_destroy.restype = None
+    R.ref_selector_fill.argtypes = [_ptr, _i64, _i64, _i64, _ptr, _ptr, _u32, _ptr, _ptr]
+    R.ref_selector_fill.restype = _i64
+    _ref = R
+    return R
+
+
+# ---------------------------------------------------------------- wrappers
+
+def unmask_schedule(total: int, steps: int, t_shift: float) -> list:
+    out = np.zeros(steps, dtype=np.int64)
+    lib().orc_unmask_schedule(total, steps, t_shift, _p(out))
+    return out.tolist()
+
+
+def build_input(text_ids, reference_codes, reference_frames, target_frames,
+                codebooks=8, mask_id=1024) -> np.ndarray:
+    text = np.ascontiguousarray(text_ids, dtype=np.uint32)
+    refc = (np.ascontiguousarray(reference_codes, dtype=np.int32)
+            if reference_frames else np.zeros(1, dtype=np.int32))
+    length = len(text) + reference_frames + target_frames
+    ids = np.zeros(codebooks * length, dtype=np.int32)
+    lib().orc_build_input(_p(text), len(text), _p(refc), reference_frames,
+                          target_frames, codebooks, mask_id, _p(ids))
+    return ids.reshape(codebooks, length)
+
+
+def score(logits: np.ndarray, frames: int, codebooks: int, vocab: int,
+          mask_id: int, guidance: float):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    pred = np.zeros(codebooks * frames, dtype=np.int32)
+    conf = np.zeros(codebooks * frames, dtype=np.float32)
+    lib().orc_score(_p(logits), frames, codebooks, vocab, mask_id, guidance,
+                    _p(pred), _p(conf))
+    return pred.reshape(codebooks, frames), conf.reshape(codebooks, frames)
+
+
+class Selector:
+    """PositionSelector (decoding.cpp:64-107) restated; `use_ref` runs the
+    reference's own compiled decoding.cpp instead."""
+
+    def __init__(self, layer_penalty: float, temperature: float, seed: int,
+                 use_ref: bool = False):
+        self._L = ref() if use_ref else lib()
+        self._pre = "ref_" if use_ref else "orc_"
+        self._h = getattr(self._L, self._pre + "selector_create")(
+            layer_penalty, temperature, seed)
+
+    def fill(self, count, codebooks, frames, prediction, confidence, mask_id,
+             codes: np.ndarray):
+        pred = np.ascontiguousarray(prediction, dtype=np.int32).ravel()
+        conf = np.ascontiguousarray(confidence, dtype=np.float32).ravel()
+        assert codes.dtype == np.int32 and codes.flags.c_contiguous
+        chosen = np.zeros(codebooks * frames, dtype=np.int64)
+        n = getattr(self._L, self._pre + "selector_fill")(
+            self._h, count, codebooks, frames, _p(pred), _p(conf), mask_id,
+            _p(codes), _p(chosen))
+        return chosen[:n].tolist()
+
+    def noise(self, total: int) -> np.ndarray:
+        assert self._pre == "orc_"
+        out = np.zeros(total, dtype=np.float32)
+        lib().orc_selector_noise(self._h, total, _p(out))
+        return out
+
+    def __del__(self):
+        try:
+            getattr(self._L, self._pre + "selector_destroy")(self._h)
+        except Exception:
+            pass
+
+
+def config_struct(cfg: dict) -> OrcConfig:
+    return OrcConfig(**{k: cfg[k] for k, _ in OrcConfig._fields_})
+
+
+class Model:
+    """The CPU model: synthetic (seeded) or from host float32 tensors."""
+
+    def __init__(self, cfg: dict, seed: int = 1234, norm_jitter: float = 0.0,
+                 host: Optional[dict] = None):
+        self.cfg = dict(cfg)
+        self._c = config_struct(cfg)
+        if host is None:
+            self._h = lib().orc_model_synthetic(ctypes.byref(self._c), seed,
+                                                norm_jitter)
+        else:
+            self._keep = host
+            layers = host["layers"]
+            ptrs = (ctypes.c_void_p * (len(layers) * 11))()
+            for l, tensors in enumerate(layers):
+                for k in range(11):
+                    ptrs[l * 11 + k] = _p(tensors[k])
+            self._ptrs = ptrs
+            self._h = lib().orc_model_from_host(
+                ctypes.byref(self._c), _p(host["text"]),
+                _p(host["audio_embeddings"]), _p(host["audio_heads"]),
+                _p(host["final_norm"]), ctypes.cast(ptrs, ctypes.c_void_p))
+
+    def forward(self, ids: np.ndarray, audio_start: int, target_frames: int,
+                emulate: bool = False) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        C, length = ids.shape
+        V = self.cfg["audio_vocab_size"]
+        out = np.zeros((2 * target_frames, C * V), dtype=np.float32)
+        lib().orc_forward(self._h, _p(ids), length, audio_start, target_frames,
+                          int(emulate), _p(out))
+        return out
+
+    def generate(self, ids, audio_start, target_frames, steps=32,
+                 guidance=2.0, t_shift=0.1, layer_penalty=5.0,
+                 temperature=0.0, seed=0, emulate=False):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        C, length = ids.shape
+        codes = np.zeros(C * target_frames, dtype=np.int32)
+        at = np.zeros(C * target_frames, dtype=np.int32)
+        lib().orc_generate(self._h, _p(ids), length, audio_start,
+                           target_frames, int(emulate), steps, guidance,
+                           t_shift, layer_penalty, temperature, seed,
+                           _p(codes), _p(at))
+        return codes.reshape(C, target_frames), at.reshape(C, target_frames)
+
+    def __del__(self):
+        try:
+            lib().orc_model_destroy(self._h)
+        except Exception:
+            pass
+
+
+def generate_from_logits(logits_trace: np.ndarray, codebooks, frames, vocab,
+                         mask_id, steps=32, guidance=2.0, t_shift=0.1,
+                         layer_penalty=5.0, temperature=0.0, seed=0):
+    trace = np.ascontiguousarray(logits_trace, dtype=np.float32)
+    executed = trace.shape[0]
+    codes = np.zeros(codebooks * frames, dtype=np.int32)
+    at = np.zeros(codebooks * frames, dtype=np.int32)
+    n = lib().orc_generate_from_logits(
+        _p(trace), executed, codebooks, frames, vocab, mask_id, steps,
+        guidance, t_shift, layer_penalty, temperature, seed, _p(codes), _p(at))
+    if n < 0:
+        raise ValueError("logits trace shorter than the executed steps")
+    return codes.reshape(codebooks, frames), at.reshape(codebooks, frames)
+
+
+def released_config(vocab_size: int = 151936) -> dict:
+    """Dimensions of the released checkpoint (tests/config_samples.hpp:15-31
+    of the reference), with the benchmark's text vocabulary."""
+    return dict(vocab_size=vocab_size, hidden_size=1024, intermediate_size=3072,
+                layers=28, heads=16, kv_heads=8, head_dim=128,
+                max_positions=40960, rms_norm_eps=1e-6, rope_theta=1e6,
+                audio_codebooks=8, audio_vocab_size=1025, audio_mask_id=1024)

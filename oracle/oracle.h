@@ -1,0 +1,119 @@
+/*
+ * ORACLE — test infrastructure, not product code.
+ *
+ * A CPU restatement of the reference's unmasking generator (gufo-extensions/
+ * omnivoice): decoding.cpp:12-107, generator.cpp:175-301,
+ * kernels/generator_kernels.hip:62-265. Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load it, and only as the checker or as the
+ * timed CPU baseline. The product (omnivoice_amd/) never links or calls it.
+ *
+ * Pinning (what fixes each function, besides the GPU comparison):
+ *   orc_unmask_schedule  - the reference fixture's three 32-step schedules,
+ *                          and oracle/_ref (the reference's decoding.cpp).
+ *   orc_build_input      - the fixture's input_ids, and oracle/_ref.
+ *   orc_selector_*       - the reference's greedy KAT (decoding_test.cpp:67-80),
+ *                          oracle/_ref with Gumbel noise, brute-force sort,
+ *                          and the std::mt19937_64 known answer.
+ *   orc_exp / orc_log    - glibc expf/logf within 2 ulp over sweeps.
+ *   orc_score            - float64 closed form per row; invariants.
+ *   orc_forward pieces   - float64 textbook formulas at tiny shapes and the
+ *                          installed transformers Qwen3 layer (fixtures).
+ *   orc_synth_*          - numpy float16 rounding; closed-form moments.
+ */
+#ifndef OMNIVOICE_ORACLE_H_
+#define OMNIVOICE_ORACLE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_config {
+  int64_t vocab_size, hidden_size, intermediate_size, layers, heads, kv_heads,
+      head_dim, max_positions;
+  float rms_norm_eps, rope_theta;
+  int64_t audio_codebooks, audio_vocab_size;
+  uint32_t audio_mask_id;
+} orc_config;
+
+/* decode.cpp */
+void orc_unmask_schedule(int64_t total, int64_t steps, float t_shift,
+                         int64_t* schedule);
+int64_t orc_build_input(const uint32_t* text_ids, int64_t text_count,
+                        const int32_t* reference_codes,
+                        int64_t reference_frames, int64_t target_frames,
+                        int64_t codebooks, uint32_t mask_id, int32_t* ids);
+float orc_exp(float x);
+float orc_log(float x);
+void orc_score(const float* logits, int64_t frames, int64_t codebooks,
+               int64_t vocab, uint32_t mask_id, float guidance,
+               int32_t* prediction, float* confidence);
+void* orc_selector_create(float layer_penalty, float temperature,
+                          uint64_t seed);
+void orc_selector_destroy(void* selector);
+int64_t orc_selector_fill(void* selector, int64_t count, int64_t codebooks,
+                          int64_t frames, const int32_t* prediction,
+                          const float* confidence, uint32_t mask_id,
+                          int32_t* codes, int64_t* chosen);
+/* Noise the selector would draw for one Fill of `total` entries. */
+void orc_selector_noise(void* selector, int64_t total, float* noise);
+uint64_t orc_mt19937_64_nth(uint64_t seed, int64_t n);
+/* Unmasking driven by given per-step logits (teacher forcing): for each
+ * executed step e, score logits_trace[e] and select. */
+int64_t orc_generate_from_logits(const float* logits_trace, int64_t executed,
+                                 int64_t codebooks, int64_t frames,
+                                 int64_t vocab, uint32_t mask_id,
+                                 int64_t steps, float guidance, float t_shift,
+                                 float layer_penalty, float temperature,
+                                 uint64_t seed, int32_t* codes,
+                                 int32_t* unmasked_at);
+
+/* synth.cpp */
+double orc_synth_normal(uint64_t seed, uint64_t tensor, uint64_t element);
+float orc_round_half(float x);
+void orc_synth_values(uint64_t seed, uint64_t tensor, uint64_t first,
+                      int64_t count, int is_norm, float jitter, float* out);
+
+/* forward.cpp */
+void* orc_model_synthetic(const orc_config* config, uint64_t seed,
+                          float norm_jitter);
+/* tensors[layer][11] in the OVG_LAYER_* order; the model copies them,
+ * rounding matrices to fp16 values. */
+void* orc_model_from_host(const orc_config* config, const float* text,
+                          const float* audio_embeddings,
+                          const float* audio_heads, const float* final_norm,
+                          const float* const* layers);
+void orc_model_destroy(void* model);
+void orc_set_threads(int threads);
+/* emulate: 0 = float32 activations, 1 = round to fp16 where the
+ * reference's GPU path rounds. logits [2F][C*V]. */
+void orc_forward(void* model, const int32_t* ids, int64_t length,
+                 int64_t audio_start, int64_t target_frames, int emulate,
+                 float* logits);
+void orc_generate(void* model, const int32_t* ids, int64_t length,
+                  int64_t audio_start, int64_t target_frames, int emulate,
+                  int64_t steps, float guidance, float t_shift,
+                  float layer_penalty, float temperature, uint64_t seed,
+                  int32_t* codes, int32_t* unmasked_at);
+
+/* kernel-level restatements (float32) */
+void orc_rmsnorm(const float* x, const float* w, float* y, int64_t rows,
+                 int64_t width, float eps);
+void orc_linear(const float* x, const float* w, float* y, int64_t rows,
+                int64_t in, int64_t out, int accumulate);
+void orc_qk_norm_rope(const float* qkv, const float* q_norm,
+                      const float* k_norm, const int32_t* positions,
+                      float* out, int64_t rows, int64_t heads,
+                      int64_t kv_heads, int64_t head_dim, float eps,
+                      float theta);
+void orc_attention(const float* qkv, float* out, int64_t rows, int64_t heads,
+                   int64_t kv_heads, int64_t head_dim,
+                   const int64_t* sequences, int64_t count, int round_p);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNIVOICE_ORACLE_H_ */

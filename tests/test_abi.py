@@ -1,0 +1,82 @@
+"""The C ABI without a GPU: the library loads and exports every function
+include/omnivoice_mi355x.h declares; its host-only helpers agree with the
+reference's fixtures and the oracle; configuration errors are reported the
+reference's way."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import omnivoice_amd as ov
+import oracle
+from conftest import ROOT
+
+
+def declared_functions():
+    with open(os.path.join(ROOT, "include", "omnivoice_mi355x.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ovg_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 19
+    lib = ctypes.CDLL(ov.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(ov.EXPORTS), set(names) ^ set(ov.EXPORTS)
+
+
+def test_schedule_and_build_match_reference_fixture(golden_cases):
+    for case in golden_cases["generate"]:
+        assert ov.unmask_schedule(8 * case["target"], 32, 0.1) == case["schedule"]
+        ids = np.array(case["input_ids"], dtype=np.int32)
+        a = case["audio_start"]
+        refc = case["reference_codes"]
+        rf = 0 if refc is None else len(refc[0])
+        built = ov.ConditionalInput.build(ids[0, :a], refc, rf, case["target"])
+        np.testing.assert_array_equal(built.ids, ids)
+        assert built.audio_start == a and built.length == ids.shape[1]
+
+
+def test_schedule_matches_oracle_everywhere():
+    for total in [1, 3, 64, 400, 2000, 3000, 8192]:
+        for steps in [1, 7, 32]:
+            for t_shift in [0.1, 0.3, 1.0]:
+                assert (ov.unmask_schedule(total, steps, t_shift) ==
+                        oracle.unmask_schedule(total, steps, t_shift))
+
+
+@pytest.mark.parametrize("tensor,norm,jitter", [(1, False, 0.0), (3, False, 0.0),
+                                                (100 + 16 * 27 + 6, False, 0.0),
+                                                (4, True, 0.0), (109, True, 0.25)])
+def test_synthetic_weights_match_oracle(tensor, norm, jitter):
+    first, count = 12345, 70001
+    mine = ov.synthetic_values(1234, tensor, first, count, norm, jitter)
+    theirs = np.zeros(count, dtype=np.float32)
+    oracle.lib().orc_synth_values(1234, tensor, first, count, int(norm), jitter,
+                                  theirs.ctypes.data)
+    np.testing.assert_array_equal(mine, theirs)
+
+
+def test_bad_config_is_rejected_with_reference_prefix():
+    cfg = ov.released_config()
+    cfg["head_dim"] = 64
+    with pytest.raises(ov.GeneratorError) as e:
+        ov.Generator.synthetic(cfg)
+    assert str(e.value) == "OmniVoice generator: head_dim must be 128"
+
+
+def test_checkpoint_directory_not_supported_yet():
+    with pytest.raises(ov.GeneratorError) as e:
+        ov.Generator.load(ov.released_config(), "/nonexistent")
+    assert str(e.value).startswith("OmniVoice generator: ")
+
+
+def test_build_input_rejects_bad_arguments():
+    ids = np.zeros(8, dtype=np.int32)
+    assert ov.lib().ovg_build_input(None, -1, None, 0, 1, 8, 1024,
+                                    ids.ctypes.data) == -1

@@ -1,0 +1,242 @@
+"""The generator through the C ABI against the oracle and the reference's
+fixtures: forward logits within tolerance of the float32 reference, the
+unmasking loop bit-exact given identical logits, and the loop's contract
+(schedule, determinism, cancellation, errors)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import omnivoice_amd as ov
+import oracle
+from conftest import GOLDEN, random_input, tiny_config
+
+pytestmark = pytest.mark.gpu
+
+# Logit parity bound against the float32 reference (the target's
+# tolerance): max-abs 2e-2 and relative L2 1e-3.
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+
+
+def _gpu_available():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not _gpu_available():
+        pytest.skip("no GPU")
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def inp(ids, audio_start, frames):
+    C, L = ids.shape
+    return ov.ConditionalInput(C, L, audio_start, frames, np.ascontiguousarray(ids))
+
+
+# ------------------------------------------------------------------ tiny model
+
+@pytest.fixture(scope="module")
+def forward_golden():
+    with open(os.path.join(GOLDEN, "forward_tiny.json")) as f:
+        return json.load(f)
+
+
+def test_forward_matches_transformers_fixture(forward_golden):
+    cfg = forward_golden["config"]
+    for case in forward_golden["cases"]:
+        gen = ov.Generator.synthetic(cfg, case["seed"], case["norm_jitter"])
+        ids = np.array(case["ids"], dtype=np.int32)
+        got = gen.forward(inp(ids, case["audio_start"], case["target"]))
+        want = np.array(case["logits"])
+        assert np.abs(got - want).max() < MAX_ABS
+        assert rel_l2(got, want) < REL_L2
+        gen.close()
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = tiny_config()
+    return cfg, ov.Generator.synthetic(cfg, 21, 0.1), oracle.Model(cfg, 21, 0.1)
+
+
+@pytest.mark.parametrize("text,ref,target,fill", [(5, 0, 40, 0.0), (20, 13, 57, 0.3),
+                                                 (1, 0, 1, 0.0), (60, 125, 200, 0.5)])
+def test_tiny_forward_matches_oracle(tiny, text, ref, target, fill):
+    cfg, gen, model = tiny
+    rng = np.random.default_rng(text + ref + target)
+    ids = random_input(rng, cfg, text, ref, target, fill)
+    got = gen.forward(inp(ids, text, target))
+    want = model.forward(ids, text, target)
+    emulated = model.forward(ids, text, target, emulate=True)
+    assert np.abs(got - want).max() < MAX_ABS
+    assert rel_l2(got, want) < REL_L2
+    # Closer still to the oracle that rounds where the GPU path rounds.
+    assert rel_l2(got, emulated) < rel_l2(got, want) * 1.5 + 1e-4
+
+
+def test_tiny_score_bit_exact_given_gpu_logits(tiny):
+    cfg, gen, _ = tiny
+    rng = np.random.default_rng(8)
+    ids = random_input(rng, cfg, 9, 0, 31, 0.2)
+    x = inp(ids, 9, 31)
+    logits = gen.forward(x)
+    pred, conf = gen.score(x, 2.0)
+    want_p, want_c = oracle.score(logits, 31, 8, 1025, 1024, 2.0)
+    np.testing.assert_array_equal(pred, want_p)
+    assert conf.tobytes() == want_c.tobytes()
+
+
+@pytest.mark.parametrize("temperature,seed", [(0.0, 0), (5.0, 42), (5.0, 7)])
+def test_generate_bit_exact_given_identical_logits(tiny, temperature, seed):
+    """Teacher forcing: the oracle scores and selects on the GPU's logits of
+    every executed step and must reproduce codes and unmask order exactly;
+    each step's GPU logits must match the oracle's forward on the same ids."""
+    cfg, gen, model = tiny
+    rng = np.random.default_rng(seed + 1)
+    text, target = 11, 45
+    ids = random_input(rng, cfg, text, 0, target)
+    x = inp(ids, text, target)
+    dec = ov.DecodingConfig(position_temperature=temperature)
+    traced = gen.generate_trace(x, dec, seed)
+    codes, at = oracle.generate_from_logits(
+        traced.logits_trace, 8, target, 1025, 1024, temperature=temperature,
+        seed=seed)
+    np.testing.assert_array_equal(traced.codes, codes)
+    np.testing.assert_array_equal(traced.unmasked_at, at)
+    # Replay the ids the loop saw and compare each step's logits.
+    current = ids.copy()
+    schedule = ov.unmask_schedule(8 * target, 32, 0.1)
+    e = 0
+    for step, count in enumerate(schedule):
+        if count == 0:
+            continue
+        if e % 8 == 0:
+            want = model.forward(current, text, target)
+            got = traced.logits_trace[e]
+            assert np.abs(got - want).max() < MAX_ABS
+            assert rel_l2(got, want) < REL_L2
+        done = (at <= step) & (at >= 0)
+        block = current[:, -target:]
+        block[done] = codes[done]
+        e += 1
+    # The captured-graph path gives the same result as the eager trace.
+    graphed = gen.generate(x, dec, seed)
+    np.testing.assert_array_equal(graphed.codes, traced.codes)
+    np.testing.assert_array_equal(graphed.unmasked_at, traced.unmasked_at)
+
+
+def test_generate_contract(tiny):
+    cfg, gen, _ = tiny
+    rng = np.random.default_rng(3)
+    text, target = 7, 64
+    x = inp(random_input(rng, cfg, text, 0, target), text, target)
+    dec = ov.DecodingConfig()
+    a = gen.generate(x, dec, 42)
+    b = gen.generate(x, dec, 42)
+    c = gen.generate(x, dec, 43)
+    np.testing.assert_array_equal(a.codes, b.codes)
+    np.testing.assert_array_equal(a.unmasked_at, b.unmasked_at)
+    assert (a.unmasked_at != c.unmasked_at).any()
+    assert ((a.codes >= 0) & (a.codes < 1024)).all()
+    schedule = ov.unmask_schedule(8 * target, 32, 0.1)
+    for step, count in enumerate(schedule):
+        assert (a.unmasked_at == step).sum() == count
+
+
+def test_generate_cancelled(tiny):
+    cfg, gen, _ = tiny
+    rng = np.random.default_rng(4)
+    x = inp(random_input(rng, cfg, 5, 0, 20), 5, 20)
+    polls = []
+
+    def cancel():
+        polls.append(1)
+        return len(polls) >= 3
+
+    with pytest.raises(ov.Cancelled) as e:
+        gen.generate(x, ov.DecodingConfig(), 1, cancelled=cancel)
+    assert str(e.value) == "cancelled"
+    assert len(polls) == 3
+    # The handle stays usable.
+    assert gen.generate(x, ov.DecodingConfig(), 1).codes.shape == (8, 20)
+
+
+def test_errors_carry_reference_prefixes(tiny):
+    cfg, gen, _ = tiny
+    ids = np.full((8, 10), 1024, dtype=np.int32)
+    ids[:, :3] = cfg["vocab_size"] + 5
+    with pytest.raises(ov.GeneratorError) as e:
+        gen.forward(inp(ids, 3, 7))
+    assert str(e.value) == "OmniVoice forward: text token outside the vocabulary"
+    with pytest.raises(ov.GeneratorError) as e:
+        gen.generate(inp(ids, 3, 7))
+    assert str(e.value).startswith("OmniVoice generation: ")
+
+
+def test_batch_matches_single_items(tiny):
+    """Packed items are independent: each item's codes follow its own
+    schedule and seed; with identical logits (teacher forcing of the batch
+    against single runs is not needed) the unmask counts per step hold."""
+    cfg, gen, _ = tiny
+    rng = np.random.default_rng(6)
+    items = [inp(random_input(rng, cfg, t, r, f), t, f)
+             for t, r, f in [(5, 0, 30), (9, 12, 45), (3, 0, 17)]]
+    dec = ov.DecodingConfig()
+    results = gen.generate_batch(items, dec, seeds=[1, 2, 3])
+    for it, res, seed in zip(items, results, [1, 2, 3]):
+        schedule = ov.unmask_schedule(8 * it.target_frames, 32, 0.1)
+        for step, count in enumerate(schedule):
+            assert (res.unmasked_at == step).sum() == count
+        single = gen.generate(it, dec, seed)
+        agree = (single.codes == res.codes).mean()
+        assert agree > 0.9, agree
+
+
+# ------------------------------------------------------------------ released shape
+
+@pytest.fixture(scope="module")
+def released():
+    cfg = ov.released_config()
+    gen = ov.Generator.synthetic(cfg, 1234)
+    model = oracle.Model(cfg, 1234)
+    yield cfg, gen, model
+    gen.close()
+
+
+@pytest.mark.parametrize("text,target", [(20, 50), (40, 100)])
+def test_released_forward_matches_float32_oracle(released, text, target):
+    """The 28-layer model at the 2 s shape and the CPU-step shape."""
+    cfg, gen, model = released
+    rng = np.random.default_rng(target)
+    ids = random_input(rng, cfg, text, 0, target)
+    got = gen.forward(inp(ids, text, target))
+    want = model.forward(ids, text, target)
+    print(f"max-abs {np.abs(got - want).max():.3e} rel-l2 {rel_l2(got, want):.3e}")
+    assert np.abs(got - want).max() < MAX_ABS
+    assert rel_l2(got, want) < REL_L2
+
+
+@pytest.mark.parametrize("shape", [(80, 0, 250), (180, 125, 375)])
+def test_released_generate_properties(released, shape):
+    cfg, gen, _ = released
+    text, ref, target = shape
+    rng = np.random.default_rng(target)
+    x = inp(random_input(rng, cfg, text, ref, target), text, target)
+    dec = ov.DecodingConfig()
+    a = gen.generate(x, dec, 42)
+    b = gen.generate(x, dec, 42)
+    np.testing.assert_array_equal(a.codes, b.codes)
+    np.testing.assert_array_equal(a.unmasked_at, b.unmasked_at)
+    assert ((a.codes >= 0) & (a.codes < 1024)).all()
+    for step, count in enumerate(ov.unmask_schedule(8 * target, 32, 0.1)):
+        assert (a.unmasked_at == step).sum() == count

@@ -1,0 +1,178 @@
+"""Device operators through the C ABI against the oracle on identical
+inputs: the CFG score and the top-k selection bit-exact, the GEMM, RMSNorm
+and attention within fp16-operand tolerances."""
+import numpy as np
+import pytest
+
+import omnivoice_amd as ov
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+# ------------------------------------------------------------------ score
+
+@pytest.mark.parametrize("frames,codebooks,vocab,guidance,scale", [
+    (50, 8, 1025, 2.0, 1.0), (250, 8, 1025, 2.0, 3.0), (7, 8, 1025, 0.0, 1.0),
+    (3, 2, 65, 3.5, 5.0), (1, 8, 1025, 2.0, 0.01), (16, 4, 1088, 1.0, 2.0)])
+def test_score_bit_exact(frames, codebooks, vocab, guidance, scale):
+    rng = np.random.default_rng(frames * 31 + vocab)
+    logits = (rng.standard_normal((2 * frames, codebooks * vocab)) * scale
+              ).astype(np.float32)
+    mask = vocab - 1
+    want_p, want_c = oracle.score(logits, frames, codebooks, vocab, mask, guidance)
+    pred = torch.zeros(codebooks * frames, dtype=torch.int32, device="cuda")
+    conf = torch.zeros(codebooks * frames, dtype=torch.float32, device="cuda")
+    ov.op_score(dev(logits), pred, conf, frames, codebooks, vocab, mask, guidance)
+    np.testing.assert_array_equal(host(pred).reshape(codebooks, frames), want_p)
+    got_c = host(conf).reshape(codebooks, frames)
+    assert got_c.tobytes() == want_c.tobytes(), np.abs(got_c - want_c).max()
+
+
+def test_score_ties_and_mask():
+    F, C, V = 4, 8, 1025
+    logits = np.zeros((2 * F, C * V), dtype=np.float32)
+    for c in range(C):
+        logits[:F, c * V + 1024] = 60.0
+        logits[:F, c * V + 33] = 2.0
+        logits[:F, c * V + 700] = 2.0
+    pred = torch.zeros(C * F, dtype=torch.int32, device="cuda")
+    conf = torch.zeros(C * F, dtype=torch.float32, device="cuda")
+    ov.op_score(dev(logits), pred, conf, F, C, V, 1024, 2.0)
+    assert (host(pred) == 33).all()
+    want_p, want_c = oracle.score(logits, F, C, V, 1024, 2.0)
+    assert host(conf).tobytes() == want_c.ravel().tobytes()
+
+
+# ------------------------------------------------------------------ select
+
+@pytest.mark.parametrize("codebooks,frames,temperature", [
+    (8, 50, 0.0), (8, 50, 5.0), (8, 250, 5.0), (8, 375, 0.0), (2, 3, 0.0),
+    (8, 2048, 5.0)])
+def test_select_bit_exact_over_a_schedule(codebooks, frames, temperature):
+    """Every step of a 32-step schedule: the GPU select (noise drawn by the
+    same mt19937_64 stream) matches the oracle's PositionSelector."""
+    rng = np.random.default_rng(frames)
+    total = codebooks * frames
+    sel = oracle.Selector(5.0, temperature, 99)
+    noise_sel = oracle.Selector(5.0, temperature, 99)
+    codes_ref = np.full(total, 1024, dtype=np.int32)
+    codes = torch.full((total,), 1024, dtype=torch.int32, device="cuda")
+    at = torch.full((total,), -1, dtype=torch.int32, device="cuda")
+    at_ref = np.full(total, -1, dtype=np.int32)
+    for step, count in enumerate(oracle.unmask_schedule(total, 32, 0.1)):
+        if count == 0:
+            continue
+        pred = rng.integers(0, 1024, size=total).astype(np.int32)
+        conf = (-rng.exponential(1.5, size=total)).astype(np.float32)
+        conf[rng.random(total) < 0.1] = np.float32(-0.75)  # ties
+        noise = noise_sel.noise(total) if temperature > 0 else np.zeros(1, np.float32)
+        for i in sel.fill(count, codebooks, frames, pred, conf, 1024, codes_ref):
+            at_ref[i] = step
+        ov.op_select(dev(pred), dev(conf), dev(noise), codes, at, codebooks,
+                     frames, count, step, 5.0, temperature, 1024)
+        np.testing.assert_array_equal(host(codes), codes_ref)
+        np.testing.assert_array_equal(host(at), at_ref)
+    assert (codes_ref != 1024).all()
+
+
+def test_select_kat():
+    """The reference's greedy known answer (decoding_test.cpp:67-80)."""
+    codes = dev(np.array([1024, 7, 1024, 1024, 1024, 1024], dtype=np.int32))
+    at = dev(np.full(6, -1, dtype=np.int32))
+    pred = dev(np.arange(10, 16, dtype=np.int32))
+    conf = dev(np.array([-0.5, -0.1, -2.0, -0.2, -0.3, -9.0], dtype=np.float32))
+    ov.op_select(pred, conf, None, codes, at, 2, 3, 2, 0, 5.0, 0.0, 1024)
+    assert host(codes).tolist() == [10, 7, 12, 1024, 1024, 1024]
+    assert host(at).tolist() == [0, -1, 0, -1, -1, -1]
+
+
+# ------------------------------------------------------------------ linear
+
+@pytest.mark.parametrize("rows,k,n,acc", [
+    (120, 1024, 4096, False), (580, 2048, 1024, True), (33, 64, 200, False),
+    (500, 1024, 8200, False), (128, 3072, 1024, True), (1, 128, 128, False),
+    (3440, 1024, 6144, False)])
+def test_linear_matches_float64(rows, k, n, acc):
+    rng = np.random.default_rng(rows + n)
+    x = rng.standard_normal((rows, k)).astype(np.float16)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    y0 = rng.standard_normal((rows, n)).astype(np.float32)
+    y = dev(y0)
+    ov.op_linear(dev(x), dev(w), y, accumulate=acc)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    if acc:
+        want += y0
+    got = host(y)
+    scale = np.sqrt(k) * 0.02
+    assert np.abs(got - want).max() < 1e-4 * scale * 10 + 1e-5
+
+
+def test_linear_is_deterministic():
+    rng = np.random.default_rng(1)
+    x = dev(rng.standard_normal((120, 3072)).astype(np.float16))
+    w = dev((rng.standard_normal((1024, 3072)) * 0.02).astype(np.float16))
+    outs = []
+    for _ in range(3):
+        y = torch.zeros((120, 1024), dtype=torch.float32, device="cuda")
+        ov.op_linear(x, w, y)
+        outs.append(host(y).tobytes())
+    assert outs[0] == outs[1] == outs[2]
+
+
+# ------------------------------------------------------------------ rmsnorm
+
+def test_rmsnorm_matches_oracle():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((37, 1024)) * 4).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    out = torch.zeros((37, 1024), dtype=torch.float16, device="cuda")
+    ov.op_rmsnorm(dev(x), dev(w), out, 1e-6)
+    want = np.zeros_like(x)
+    oracle.lib().orc_rmsnorm(x.ctypes.data, w.ctypes.data, want.ctypes.data,
+                             37, 1024, 1e-6)
+    got = host(out).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-3)
+
+
+# ------------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("seqs", [[(0, 330), (336, 250)], [(0, 1), (8, 31)],
+                                  [(0, 680), (680, 375)], [(0, 33)]])
+def test_attention_matches_oracle(seqs):
+    rng = np.random.default_rng(len(seqs) + seqs[-1][1])
+    heads, kv = 16, 8
+    rows = seqs[-1][0] + seqs[-1][1]
+    width = (heads + 2 * kv) * 128
+    qkv = (rng.standard_normal((rows, width)) * 1.5).astype(np.float16)
+    out = torch.zeros((rows, heads * 128), dtype=torch.float16, device="cuda")
+    ov.op_attention(dev(qkv), out, heads, kv, seqs)
+    want = np.zeros((rows, heads * 128), dtype=np.float32)
+    s = np.array(seqs, dtype=np.int64).ravel()
+    q32 = qkv.astype(np.float32)
+    oracle.lib().orc_attention(q32.ctypes.data, want.ctypes.data, rows, heads,
+                               kv, 128, s.ctypes.data, len(seqs), 0)
+    got = host(out).astype(np.float32)
+    covered = np.zeros(rows, dtype=bool)
+    for first, length in seqs:
+        covered[first:first + length] = True
+    err = np.abs(got[covered] - want[covered])
+    assert err.max() < 1.5e-2, err.max()
+    assert np.linalg.norm(got[covered] - want[covered]) / np.linalg.norm(want[covered]) < 3e-3

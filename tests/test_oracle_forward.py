@@ -1,0 +1,127 @@
+"""Pins the oracle's forward pass: each piece against a float64 formulation
+of the textbook operation at tiny shapes, and the whole forward against the
+committed fixture computed with transformers' Qwen3 decoder layers."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import GOLDEN
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def test_rmsnorm_matches_float64():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((9, 256)).astype(np.float32) * 3
+    w = rng.standard_normal(256).astype(np.float32)
+    y = np.zeros_like(x)
+    oracle.lib().orc_rmsnorm(_p(x), _p(w), _p(y), 9, 256, 1e-6)
+    x64 = x.astype(np.float64)
+    want = w * x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(y, want, rtol=2e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,k,n", [(7, 72, 13), (16, 128, 64), (5, 1024, 9)])
+def test_linear_matches_float64(rows, k, n):
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    y = np.ones((rows, n), dtype=np.float32)
+    oracle.lib().orc_linear(_p(x), _p(w), _p(y), rows, k, n, 1)
+    want = 1.0 + x.astype(np.float64) @ w.astype(np.float64).T
+    np.testing.assert_allclose(y, want, rtol=1e-4, atol=1e-4)
+
+
+def test_qk_norm_rope_matches_complex_rotation():
+    """Rotate-half RoPE is multiplication of (x_i + i x_{i+64}) by
+    exp(i pos theta^(-2i/d)); q and k heads are RMS-normalised with their own
+    weights, v heads pass through."""
+    rng = np.random.default_rng(1)
+    heads, kv, d, rows = 4, 2, 128, 6
+    width = (heads + 2 * kv) * d
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    pos = np.array([0, 1, 5, 77, 300, 4000], dtype=np.int32)
+    out = np.zeros_like(x)
+    oracle.lib().orc_qk_norm_rope(_p(x), _p(qn), _p(kn), _p(pos), _p(out),
+                                  rows, heads, kv, d, 1e-6, 1e6)
+    half = d // 2
+    # Hugging Face forms inv_freq and the angle in float32 (the reference's
+    # kernel does the same); the rotation itself is then exact.
+    freq = (np.float32(1.0) / np.float32(1e6) ** (np.arange(half, dtype=np.float32)
+                                                 * np.float32(2.0 / d)))
+    for r in range(rows):
+        for s in range(heads + 2 * kv):
+            v = x[r, s * d:(s + 1) * d].astype(np.float64)
+            got = out[r, s * d:(s + 1) * d]
+            if s >= heads + kv:
+                np.testing.assert_array_equal(got, x[r, s * d:(s + 1) * d])
+                continue
+            w = qn if s < heads else kn
+            v = w * v / np.sqrt((v ** 2).mean() + 1e-6)
+            angle = (np.float32(pos[r]) * freq).astype(np.float64)
+            z = (v[:half] + 1j * v[half:]) * np.exp(1j * angle)
+            want = np.concatenate([z.real, z.imag])
+            # One float32 ulp of inv_freq or of the angle moves the angle by
+            # up to ~1e-7 * pos rad; a wrong sign, half or frequency is O(1).
+            atol = 3e-5 + 3e-7 * pos[r] * np.abs(v).max()
+            np.testing.assert_allclose(got, want, rtol=0, atol=atol)
+
+
+def test_attention_matches_float64_with_gqa():
+    rng = np.random.default_rng(4)
+    heads, kv, d = 4, 2, 128
+    seqs = [(0, 11), (16, 5)]
+    rows = 21
+    width = (heads + 2 * kv) * d
+    qkv = rng.standard_normal((rows, width)).astype(np.float32)
+    out = np.zeros((rows, heads * d), dtype=np.float32)
+    s = np.array(seqs, dtype=np.int64).ravel()
+    oracle.lib().orc_attention(_p(qkv), _p(out), rows, heads, kv, d, _p(s),
+                               len(seqs), 0)
+    x = qkv.astype(np.float64)
+    for first, length in seqs:
+        for h in range(heads):
+            g = h // (heads // kv)
+            q = x[first:first + length, h * d:(h + 1) * d]
+            k = x[first:first + length, (heads + g) * d:(heads + g + 1) * d]
+            v = x[first:first + length, (heads + kv + g) * d:(heads + kv + g + 1) * d]
+            a = q @ k.T / np.sqrt(d)
+            p = np.exp(a - a.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            np.testing.assert_allclose(out[first:first + length, h * d:(h + 1) * d],
+                                       p @ v, rtol=1e-4, atol=1e-5)
+
+
+def test_forward_matches_transformers_fixture():
+    with open(os.path.join(GOLDEN, "forward_tiny.json")) as f:
+        golden = json.load(f)
+    cfg = golden["config"]
+    for case in golden["cases"]:
+        model = oracle.Model(cfg, seed=case["seed"],
+                             norm_jitter=case["norm_jitter"])
+        ids = np.array(case["ids"], dtype=np.int32)
+        got = model.forward(ids, case["audio_start"], case["target"])
+        want = np.array(case["logits"])
+        assert np.abs(got - want).max() < 5e-6
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) < 5e-6
+
+
+def test_emulated_fp16_stays_close_to_float32():
+    """Rounding at the reference's fp16 points moves the tiny model's logits
+    by far less than the parity tolerance."""
+    with open(os.path.join(GOLDEN, "forward_tiny.json")) as f:
+        golden = json.load(f)
+    case = golden["cases"][0]
+    model = oracle.Model(golden["config"], seed=case["seed"],
+                         norm_jitter=case["norm_jitter"])
+    ids = np.array(case["ids"], dtype=np.int32)
+    a = model.forward(ids, case["audio_start"], case["target"], emulate=False)
+    b = model.forward(ids, case["audio_start"], case["target"], emulate=True)
+    assert 0 < np.abs(a - b).max() < 5e-3

@@ -5,18 +5,22 @@
 // 161-189). Scores never leave registers.
 //
 // A work-group takes one tile of 32 queries of one sequence and one key/value
-// head g; its waves are the query heads of g's group (2 for 16 q / 8 kv), so
-// each K/V tile is staged in LDS once for the whole group (no GQA repeat).
+// head g. Its 2 x GROUP waves are the GROUP query heads of g times two key
+// halves: keys are staged in LDS as pairs of 32-key tiles (K [32][128] and
+// V^T [128][32] each), the first tile of a pair for key-half 0, the second
+// for key-half 1, so each K/V tile is read from memory once for the whole
+// head group (no GQA repeat). The next pair is prefetched into registers
+// while the current one is used (double-buffered LDS, one barrier per pair).
+// At the end the two key halves' online-softmax states merge through LDS.
 //
 // Scores are formed transposed, S^T = K Q^T (keys as MFMA rows, queries as
 // columns), so that every lane owns one query column: the running max and
-// sum of the online softmax are per-lane values combined with the partner
-// lane l ^ 32 only. The value product is likewise transposed,
-// O^T = V^T P^T: P^T is the score accumulator itself converted to fp16 (the
-// k index order of the MFMA is permuted to the accumulator's row order, and
-// V^T is read from LDS in the same permuted order), so probabilities never
-// move between lanes. V^T comes pre-transposed from the q/k/v GEMM's
-// epilogue ([kv head][dim][row]).
+// sum are per-lane values combined with the partner lane l ^ 32 only. The
+// value product is likewise transposed, O^T = V^T P^T: P^T is the score
+// accumulator itself converted to fp16 (the MFMA's k order is permuted to
+// the accumulator's row order, and V^T is read from LDS in the same order),
+// so probabilities never move between lanes. V^T comes pre-transposed from
+// the q/k/v GEMM's epilogue ([kv head][dim][row]).
 #include "kernels.hpp"
 
 namespace ovg {
@@ -26,18 +30,26 @@ constexpr int kKTile = 32;
 constexpr int kHeadDim = 128;
 constexpr int kKPitch = kHeadDim + 8;  // halves per key row in LDS
 constexpr int kVPitch = kKTile + 8;    // halves per dim row of V^T in LDS
+constexpr int kKHalves = kKTile * kKPitch;
+constexpr int kVHalves = kHeadDim * kVPitch;
+constexpr int kTileHalves = kKHalves + kVHalves;  // one staged key tile
+constexpr int kChunksPerTile = 2 * kKTile * kHeadDim / 8;  // K + V^T, 16 B
 
 template <int GROUP>
-__global__ __launch_bounds__(GROUP * 64) void AttentionKernel(
+__global__ __launch_bounds__(GROUP * 128) void AttentionKernel(
     AttentionParams p) {
-  __shared__ __align__(16) half_t ks[kKTile * kKPitch];
-  __shared__ __align__(16) half_t vs[kHeadDim * kVPitch];
+  constexpr int kThreads = GROUP * 128;
+  constexpr int kChunks = 2 * kChunksPerTile / kThreads;  // per thread per pair
+  // Two buffers of a tile pair; the merge area reuses them.
+  __shared__ __align__(16) half_t lds[2 * 2 * kTileHalves];
   const AttentionWork work = p.work[blockIdx.x];
   const int g = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int head = g * GROUP + wave;
+  const int head_local = wave % GROUP;
+  const int key_half = wave / GROUP;
+  const int head = g * GROUP + head_local;
   const int half_id = lane >> 5;
   const int col = lane & 31;
 
@@ -62,72 +74,134 @@ __global__ __launch_bounds__(GROUP * 64) void AttentionKernel(
   const half_t* kbase = p.qk + (p.heads + g) * kHeadDim;
   const half_t* vbase = p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt;
   const int tiles = (work.seq_length + kKTile - 1) / kKTile;
-  for (int t = 0; t < tiles; ++t) {
-    const int key0 = work.seq_begin + t * kKTile;
-    // Stage K [32 keys][128] and V^T [128 dims][32 keys] (512 chunks each).
-    for (int c = tid; c < kKTile * kHeadDim / 8; c += GROUP * 64) {
-      const int row = c >> 4, c8 = (c & 15) * 8;
-      *reinterpret_cast<half8*>(ks + row * kKPitch + c8) =
-          *reinterpret_cast<const half8*>(
-              kbase + static_cast<size_t>(key0 + row) * p.ld_qk + c8);
-      const int d = c >> 2, k8 = (c & 3) * 8;
-      *reinterpret_cast<half8*>(vs + d * kVPitch + k8) =
-          *reinterpret_cast<const half8*>(
-              vbase + static_cast<size_t>(d) * p.ldvt + key0 + k8);
-    }
-    __syncthreads();
+  const int pairs = (tiles + 1) / 2;
 
-    floatx16 s = floatx16{};
+  // Chunk c of a pair: tile c / kChunksPerTile; within a tile the first 512
+  // chunks are K rows (16 per key), the rest V^T rows (4 per dim).
+  half8 staged[kChunks];
+  auto load = [&](int pair) {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const half8 kf = *reinterpret_cast<const half8*>(
-          ks + col * kKPitch + kk * 16 + half_id * 8);
-      s = Mfma32(kf, qf[kk], s);
-    }
-    // Lane holds keys 8 (r / 4) + 4 half_id + r % 4 of its query column.
-    const int valid_keys = work.seq_length - t * kKTile;
-    float tile_max = -__builtin_inff();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = 8 * (r / 4) + 4 * half_id + (r & 3);
-      s[r] = key < valid_keys ? s[r] * p.scale_log2 : -__builtin_inff();
-      tile_max = fmaxf(tile_max, s[r]);
-    }
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-    const float new_max = fmaxf(run_max, tile_max);
-    const float alpha = __builtin_amdgcn_exp2f(run_max - new_max);
-    run_max = new_max;
-    float psum = 0.0F;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = __builtin_amdgcn_exp2f(s[r] - new_max);
-      psum += s[r];
-    }
-    run_sum = run_sum * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-      ot[dt] *= alpha;
-    // P^T operand for keys 16 j2 .. 16 j2 + 15: slot e <-> accumulator
-    // element 8 j2 + e, i.e. key 16 j2 + (e < 4 ? 4 h + e : 8 + 4 h + e - 4).
-#pragma unroll
-    for (int j2 = 0; j2 < 2; ++j2) {
-      half8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        pb[e] = static_cast<half_t>(s[8 * j2 + e]);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const half_t* vrow = vs + (dt * 32 + col) * kVPitch + 16 * j2 + 4 * half_id;
-        const half4 lo = *reinterpret_cast<const half4*>(vrow);
-        const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
-        const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        ot[dt] = Mfma32(va, pb, ot[dt]);
+    for (int j = 0; j < kChunks; ++j) {
+      const int c = tid + j * kThreads;
+      const int t = 2 * pair + c / kChunksPerTile;
+      const int ci = c % kChunksPerTile;
+      const int key0 = work.seq_begin + t * kKTile;
+      if (t >= tiles)
+        continue;
+      if (ci < kChunksPerTile / 2) {
+        staged[j] = *reinterpret_cast<const half8*>(
+            kbase + static_cast<size_t>(key0 + (ci >> 4)) * p.ld_qk + (ci & 15) * 8);
+      } else {
+        const int cv = ci - kChunksPerTile / 2;
+        staged[j] = *reinterpret_cast<const half8*>(
+            vbase + static_cast<size_t>(cv >> 2) * p.ldvt + key0 + (cv & 3) * 8);
       }
     }
+  };
+  auto store = [&](int pair, int buffer) {
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      const int c = tid + j * kThreads;
+      const int slot = c / kChunksPerTile;
+      const int ci = c % kChunksPerTile;
+      if (2 * pair + slot >= tiles)
+        continue;
+      half_t* tile_lds = lds + (buffer * 2 + slot) * kTileHalves;
+      if (ci < kChunksPerTile / 2) {
+        *reinterpret_cast<half8*>(tile_lds + (ci >> 4) * kKPitch + (ci & 15) * 8) =
+            staged[j];
+      } else {
+        const int cv = ci - kChunksPerTile / 2;
+        *reinterpret_cast<half8*>(tile_lds + kKHalves + (cv >> 2) * kVPitch +
+                                  (cv & 3) * 8) = staged[j];
+      }
+    }
+  };
+
+  load(0);
+  store(0, 0);
+  __syncthreads();
+  for (int pair = 0; pair < pairs; ++pair) {
+    if (pair + 1 < pairs)
+      load(pair + 1);
+    const int t = 2 * pair + key_half;
+    if (t < tiles) {
+      const half_t* ks = lds + ((pair & 1) * 2 + key_half) * kTileHalves;
+      const half_t* vs = ks + kKHalves;
+      floatx16 s = floatx16{};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const half8 kf = *reinterpret_cast<const half8*>(
+            ks + col * kKPitch + kk * 16 + half_id * 8);
+        s = Mfma32(kf, qf[kk], s);
+      }
+      // Lane holds keys 8 (r / 4) + 4 half_id + r % 4 of its query column.
+      const int valid_keys = work.seq_length - t * kKTile;
+      float tile_max = -__builtin_inff();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r / 4) + 4 * half_id + (r & 3);
+        s[r] = key < valid_keys ? s[r] * p.scale_log2 : -__builtin_inff();
+        tile_max = fmaxf(tile_max, s[r]);
+      }
+      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+      const float new_max = fmaxf(run_max, tile_max);
+      const float alpha = __builtin_amdgcn_exp2f(run_max - new_max);
+      run_max = new_max;
+      float psum = 0.0F;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - new_max);
+        psum += s[r];
+      }
+      run_sum = run_sum * alpha + psum;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        ot[dt] *= alpha;
+      // P^T operand for keys 16 j2 .. 16 j2 + 15: slot e <-> accumulator
+      // element 8 j2 + e, i.e. key 16 j2 + (e < 4 ? 4 h + e : 8 + 4 h + e - 4).
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) {
+        half8 pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pb[e] = static_cast<half_t>(s[8 * j2 + e]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const half_t* vrow = vs + (dt * 32 + col) * kVPitch + 16 * j2 + 4 * half_id;
+          const half4 lo = *reinterpret_cast<const half4*>(vrow);
+          const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
+          const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          ot[dt] = Mfma32(va, pb, ot[dt]);
+        }
+      }
+    }
+    if (pair + 1 < pairs)
+      store(pair + 1, (pair + 1) & 1);
     __syncthreads();
   }
 
-  const float total = run_sum + __shfl_xor(run_sum, 32);
+  // Merge the key halves: half 1 leaves (max, sum, O) per lane in LDS.
+  float* merge = reinterpret_cast<float*>(lds);
+  float* mine = merge + (head_local * 64 + lane) * 66;
+  if (key_half == 1) {
+    mine[0] = run_max;
+    mine[1] = run_sum;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        mine[2 + dt * 16 + r] = ot[dt][r];
+  }
+  __syncthreads();
+  if (key_half == 1)
+    return;
+  const float other_max = mine[0];
+  const float new_max = fmaxf(run_max, other_max);
+  const float a0 = __builtin_amdgcn_exp2f(run_max - new_max);
+  const float a1 = __builtin_amdgcn_exp2f(other_max - new_max);
+  const float sum = run_sum * a0 + mine[1] * a1;
+  const float total = sum + __shfl_xor(sum, 32);
   const float inverse = 1.0F / total;
   if (col >= work.q_count)
     return;
@@ -138,10 +212,13 @@ __global__ __launch_bounds__(GROUP * 64) void AttentionKernel(
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const half4 v = {static_cast<half_t>(ot[dt][4 * q] * inverse),
-                       static_cast<half_t>(ot[dt][4 * q + 1] * inverse),
-                       static_cast<half_t>(ot[dt][4 * q + 2] * inverse),
-                       static_cast<half_t>(ot[dt][4 * q + 3] * inverse)};
+      half4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * q + e;
+        v[e] = static_cast<half_t>(
+            (ot[dt][r] * a0 + mine[2 + dt * 16 + r] * a1) * inverse);
+      }
       *reinterpret_cast<half4*>(out + dt * 32 + 8 * q + 4 * half_id) = v;
     }
 }
@@ -158,13 +235,13 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   const dim3 grid(p.work_count, p.kv_heads);
   switch (group) {
     case 1:
-      hipLaunchKernelGGL(AttentionKernel<1>, grid, dim3(64), 0, stream, p);
+      AttentionKernel<1><<<grid, dim3(128), 0, stream>>>(p);
       break;
     case 2:
-      hipLaunchKernelGGL(AttentionKernel<2>, grid, dim3(128), 0, stream, p);
+      AttentionKernel<2><<<grid, dim3(256), 0, stream>>>(p);
       break;
     case 4:
-      hipLaunchKernelGGL(AttentionKernel<4>, grid, dim3(256), 0, stream, p);
+      AttentionKernel<4><<<grid, dim3(512), 0, stream>>>(p);
       break;
     default:
       throw Error("attention: query heads per kv head must be 1, 2 or 4");

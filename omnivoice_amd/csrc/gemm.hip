@@ -4,186 +4,222 @@
 // that followed them, kernels/generator_kernels.hip:102-159, 191-200).
 //
 // Y[m][n] = sum_k X[m][k] W[n][k]: both operands are K-contiguous, so a
-// lane's eight consecutive k values are one 16-byte load, exactly the
-// operand a v_mfma_f32_32x32x16_f16 lane supplies.
+// lane's eight consecutive k values are one 16-byte fragment of a
+// v_mfma_f32_32x32x16_f16.
 //
-// Tile: BM = 128 * FM rows x BN = 128 columns x BK = 64, 256 threads as 4
-// waves stacked along M; each wave owns FM x 4 accumulators of 32 x 32, so a
-// wave holds complete 128-column rows. That is what lets the epilogues work
-// in registers: a Qwen3 head is one 128-column tile (per-head RMSNorm is a
-// 32-lane butterfly, and rotate-half pairs i, i + 64 sit in the same lane in
-// accumulators fn and fn + 2), and the SwiGLU gate/up pair of a column sits
-// in accumulators fn and fn + 2 of the interleaved weight tile.
+// One work-group computes a 128 x 128 output tile with 8 waves: two groups
+// of four split each 64-wide K step between them (substeps 0-1 and 2-3), and
+// inside a group the waves form a 2 x 2 grid of 64 x 64 sub-tiles. Two waves
+// per SIMD hide each other's LDS latency, and 64 x 64 wave tiles read 4 KB
+// of LDS per 4 MFMAs; gfx950's LDS delivers ~180 B/clk/CU with 8 waves but
+// only ~100 with 4, which is what bounded a 4-wave tile.
 //
-// Operands are staged global -> registers -> LDS (row pitch BK + 8 halves,
-// so the 16-byte fragment reads of 32 consecutive rows hit distinct banks),
-// double-buffered with one barrier per K step.
+// Operands go global -> LDS by DMA (global_load_lds_dwordx4) through a
+// 2- to 4-stage ring of 32 KB stages, no registers involved; LDS rows are
+// 128 bytes with an XOR swizzle of the 16-byte chunks.
 //
-// Split-K: when the output tiles alone cannot fill the 256 CUs, the K range
-// is split; each work-group stores its partial tile in accumulator order and
-// bumps the tile's counter, and the last one to arrive adds the partials in
-// split order 0, 1, ... (a fixed order, whichever group arrives last), runs
-// the epilogue and resets the counter to zero for the next launch.
+// Epilogue: the two groups' accumulators are summed into an fp32 tile in
+// LDS (group 0 + group 1, a fixed order), then all 8 waves walk the tile by
+// rows: plain or residual-accumulating fp32 stores; the q/k/v epilogue (a
+// Qwen3 head is one 128-column tile: per-head RMSNorm is one wave
+// reduction, rotate-half pairs are columns l and l + 64 of lane l, value
+// heads are written transposed); or SwiGLU over the interleaved gate/up
+// weight tile (columns l and l + 64 are the gate and up of one output).
+//
+// Split-K (for small M only): work-groups store their reduced tile as a
+// partial and a second launch sums the partials in split order 0, 1, ...
+// and runs the same epilogue; the kernel boundary publishes the partials to
+// every XCD.
 //
 // Work-groups are dispatched round-robin over the 8 XCDs; the block index is
-// remapped so that each XCD receives a contiguous run of tiles, and tiles
-// are ordered M-fastest, so the groups sharing a weight tile share an L2.
+// remapped so that each XCD receives a contiguous run of tiles, ordered
+// M-fastest, so the groups sharing a weight tile share an L2.
 #include "kernels.hpp"
 
 namespace ovg {
 namespace {
 
+constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 64;
-constexpr int kPitch = kBK + 8;  // halves per LDS row
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kXcds = 8;
+constexpr int kABytes = kBM * kBK * 2;  // one stage of A: 16 KB
+constexpr int kBBytes = kBN * kBK * 2;
+constexpr int kStageBytes = kABytes + kBBytes;
+constexpr int kAInstr = kABytes / 1024 / 8;  // 1 KB DMA blocks per wave
+constexpr int kBInstr = kBBytes / 1024 / 8;
+constexpr int kLoads = kAInstr + kBInstr;  // DMA instructions per stage
+constexpr int kPitch = kBN + 4;            // floats per row of the fp32 tile
+constexpr int kTileFloats = kBM * kBN;
+constexpr int kEpilogueBytes = kBM * kPitch * 4;
 
-template <int FM>
-struct Tile {
-  static constexpr int kBM = 128 * FM;
-  static constexpr int kAChunks = kBM * kBK / 8 / kThreads;  // 16-B chunks
-  static constexpr int kBChunks = kBN * kBK / 8 / kThreads;
-  static constexpr int kStageHalves = (kBM + kBN) * kPitch;
-  static constexpr int kLdsBytes = 2 * kStageHalves * 2;
-  static constexpr int kTileFloats = kBM * kBN;
-};
-
-__device__ __forceinline__ half8 LoadChunk(const half_t* p, bool valid) {
-  if (!valid)
-    return half8{0, 0, 0, 0, 0, 0, 0, 0};
-  return *reinterpret_cast<const half8*>(p);
+template <int STAGES>
+constexpr int LdsBytes() {
+  return STAGES * kStageBytes > kEpilogueBytes ? STAGES * kStageBytes
+                                               : kEpilogueBytes;
 }
 
-template <int FM>
-__device__ __forceinline__ void Epilogue32(const GemmParams& p,
-                                           floatx16 (&acc)[FM][4], int m0,
-                                           int n0, bool accumulate) {
+// LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
+__device__ __forceinline__ uint32_t LdsAddress(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) unsigned char*)(p)));
+}
+
+// Operand stages are [rows][64 halves]: 128-byte rows, no padding. The
+// 16-byte chunk c of row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1):
+// the 32 rows a fragment read touches then fall on distinct banks in both
+// 8-lane (128-byte) and 16-lane (256-byte) LDS phases. Its own inverse.
+__device__ __forceinline__ int Swizzle(int row, int chunk) {
+  return chunk ^ (row & 7) ^ ((row >> 3) & 1);
+}
+
+// One wave-wide DMA of 64 x 16 bytes from global memory straight into LDS:
+// lane l's 16 bytes land at lds_addr + 16 l. Inline assembly because the
+// compiler's wait-count pass cannot tell which stage buffer such a load
+// writes and would wait for every load in flight before any LDS read, which
+// serialises the ring; the kernel waits explicitly instead.
+__device__ __forceinline__ void DmaToLds(const void* src, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
+      : "memory", "m0");
+}
+
+// Waits until at most N of this wave's vector memory loads are in flight.
+template <int N>
+__device__ __forceinline__ void WaitLoads() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Barrier without the memory fence __syncthreads() carries (that fence
+// would wait for every DMA in flight); the empty asm statements keep the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void StageBarrier() {
+  asm volatile("" : : : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" : : : "memory");
+}
+
+// ------------------------------------------------------------- epilogues
+// All read the summed fp32 tile from LDS ([kBM][kPitch]) with 512 threads.
+
+__device__ __forceinline__ void StoreRows(const GemmParams& p,
+                                          const float* tile, int m0, int n0,
+                                          bool accumulate) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wave * FM * 32 + fm * 32 + 8 * (r / 4) +
-                    4 * (lane >> 5) + (r & 3);
-      if (m >= p.m)
-        continue;
-      float* row = p.y + static_cast<size_t>(m) * p.ldc;
-#pragma unroll
-      for (int fn = 0; fn < 4; ++fn) {
-        const int n = n0 + fn * 32 + (lane & 31);
-        if (n < p.n) {
-          if (accumulate)
-            row[n] += acc[fm][fn][r];
-          else
-            row[n] = acc[fm][fn][r];
-        }
+  for (int r = wave; r < kBM; r += kThreads / 64) {
+    const int m = m0 + r;
+    if (m >= p.m)
+      break;
+    const int n = n0 + 2 * lane;
+    const float2 v = *reinterpret_cast<const float2*>(tile + r * kPitch + 2 * lane);
+    float* dst = p.y + static_cast<size_t>(m) * p.ldc + n;
+    if (n + 1 < p.n && (p.ldc & 1) == 0) {
+      float2* d2 = reinterpret_cast<float2*>(dst);
+      if (accumulate) {
+        float2 o = *d2;
+        o.x += v.x;
+        o.y += v.y;
+        *d2 = o;
+      } else {
+        *d2 = v;
       }
+    } else {
+      if (n < p.n)
+        dst[0] = accumulate ? dst[0] + v.x : v.x;
+      if (n + 1 < p.n)
+        dst[1] = accumulate ? dst[1] + v.y : v.y;
     }
   }
 }
 
-template <int FM>
-__device__ __forceinline__ void EpilogueQkv(const GemmParams& p,
-                                            floatx16 (&acc)[FM][4], int m0,
-                                            int slot) {
+__device__ __forceinline__ void QkvRows(const GemmParams& p, const float* tile,
+                                        int m0, int slot) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int col = lane & 31;
   if (slot < p.heads + p.kv_heads) {
     const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
-    const float w0 = weight[col], w1 = weight[col + 32];
-    const float w2 = weight[col + 64], w3 = weight[col + 96];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float v0 = acc[fm][0][r], v1 = acc[fm][1][r];
-        const float v2 = acc[fm][2][r], v3 = acc[fm][3][r];
-        float squares = v0 * v0 + v1 * v1 + v2 * v2 + v3 * v3;
-#pragma unroll
-        for (int offset = 16; offset > 0; offset /= 2)
-          squares += __shfl_xor(squares, offset);
-        const int m = m0 + wave * FM * 32 + fm * 32 + 8 * (r / 4) +
-                      4 * (lane >> 5) + (r & 3);
-        if (m >= p.m)
-          continue;
-        const float scale = rsqrtf(squares * (1.0F / 128.0F) + p.eps);
-        const float2* rope = p.rope + static_cast<size_t>(p.positions[m]) * 64;
-        const float2 cs0 = rope[col], cs1 = rope[col + 32];
-        const float a0 = w0 * (v0 * scale), b0 = w2 * (v2 * scale);
-        const float a1 = w1 * (v1 * scale), b1 = w3 * (v3 * scale);
-        half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
-        out[col] = static_cast<half_t>(a0 * cs0.x - b0 * cs0.y);
-        out[col + 64] = static_cast<half_t>(b0 * cs0.x + a0 * cs0.y);
-        out[col + 32] = static_cast<half_t>(a1 * cs1.x - b1 * cs1.y);
-        out[col + 96] = static_cast<half_t>(b1 * cs1.x + a1 * cs1.y);
-      }
+    const float w0 = weight[lane], w1 = weight[lane + 64];
+    for (int r = wave; r < kBM; r += kThreads / 64) {
+      const int m = m0 + r;
+      if (m >= p.m)
+        break;
+      const float v0 = tile[r * kPitch + lane];
+      const float v1 = tile[r * kPitch + lane + 64];
+      const float squares = WaveSum(v0 * v0 + v1 * v1);
+      const float scale = rsqrtf(squares * (1.0F / 128.0F) + p.eps);
+      const float2 cs = p.rope[static_cast<size_t>(p.positions[m]) * 64 + lane];
+      const float a = w0 * (v0 * scale);
+      const float b = w1 * (v1 * scale);
+      half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
+      out[lane] = static_cast<half_t>(a * cs.x - b * cs.y);
+      out[lane + 64] = static_cast<half_t>(b * cs.x + a * cs.y);
     }
     return;
   }
   // Value heads: V^T[g][d][row], four consecutive rows per 8-byte store.
   const int g = slot - p.heads - p.kv_heads;
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = m0 + wave * FM * 32 + fm * 32 + 8 * q + 4 * (lane >> 5);
-      if (m >= p.m)
-        continue;
-#pragma unroll
-      for (int fn = 0; fn < 4; ++fn) {
-        const int d = fn * 32 + col;
-        half_t* out = p.vt + static_cast<size_t>(g * 128 + d) * p.ldvt + m;
-        const half4 v = {static_cast<half_t>(acc[fm][fn][4 * q]),
-                         static_cast<half_t>(acc[fm][fn][4 * q + 1]),
-                         static_cast<half_t>(acc[fm][fn][4 * q + 2]),
-                         static_cast<half_t>(acc[fm][fn][4 * q + 3])};
-        if (m + 3 < p.m) {
-          *reinterpret_cast<half4*>(out) = v;
-        } else {
-          for (int e = 0; e < 4 && m + e < p.m; ++e)
-            out[e] = v[e];
-        }
-      }
+  const int d = threadIdx.x & 127;
+  half_t* out = p.vt + static_cast<size_t>(g * 128 + d) * p.ldvt;
+  for (int q = threadIdx.x >> 7; q < kBM / 4; q += kThreads / 128) {
+    const int m = m0 + 4 * q;
+    if (m >= p.m)
+      break;
+    const half4 v = {static_cast<half_t>(tile[(4 * q) * kPitch + d]),
+                     static_cast<half_t>(tile[(4 * q + 1) * kPitch + d]),
+                     static_cast<half_t>(tile[(4 * q + 2) * kPitch + d]),
+                     static_cast<half_t>(tile[(4 * q + 3) * kPitch + d])};
+    if (m + 3 < p.m) {
+      *reinterpret_cast<half4*>(out + m) = v;
+    } else {
+      for (int e = 0; e < 4 && m + e < p.m; ++e)
+        out[m + e] = v[e];
     }
   }
 }
 
-template <int FM>
-__device__ __forceinline__ void EpilogueSwiGlu(const GemmParams& p,
-                                               floatx16 (&acc)[FM][4], int m0,
-                                               int tile_n) {
+__device__ __forceinline__ void SwiGluRows(const GemmParams& p,
+                                           const float* tile, int m0,
+                                           int tile_n) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int col = lane & 31;
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wave * FM * 32 + fm * 32 + 8 * (r / 4) +
-                    4 * (lane >> 5) + (r & 3);
-      if (m >= p.m)
-        continue;
-      half_t* out = p.act + static_cast<size_t>(m) * p.ldh + tile_n * 64;
-#pragma unroll
-      for (int fn = 0; fn < 2; ++fn) {
-        const float g = acc[fm][fn][r];
-        const float u = acc[fm][fn + 2][r];
-        out[fn * 32 + col] = static_cast<half_t>(g / (1.0F + __expf(-g)) * u);
-      }
-    }
+  for (int r = wave; r < kBM; r += kThreads / 64) {
+    const int m = m0 + r;
+    if (m >= p.m)
+      break;
+    const float g = tile[r * kPitch + lane];
+    const float u = tile[r * kPitch + lane + 64];
+    p.act[static_cast<size_t>(m) * p.ldh + tile_n * 64 + lane] =
+        static_cast<half_t>(g / (1.0F + __expf(-g)) * u);
   }
 }
 
-template <int FM, Epilogue EPI>
+template <Epilogue EPI>
+__device__ __forceinline__ void TileEpilogue(const GemmParams& p,
+                                             const float* tile, int tile_m,
+                                             int tile_n) {
+  const int m0 = tile_m * kBM;
+  if constexpr (EPI == Epilogue::kStore)
+    StoreRows(p, tile, m0, tile_n * kBN, false);
+  else if constexpr (EPI == Epilogue::kAccumulate)
+    StoreRows(p, tile, m0, tile_n * kBN, true);
+  else if constexpr (EPI == Epilogue::kQkvRope)
+    QkvRows(p, tile, m0, tile_n);
+  else
+    SwiGluRows(p, tile, m0, tile_n);
+}
+
+// ------------------------------------------------------------- main kernel
+
+template <int STAGES, Epilogue EPI>
 __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
                                                        int tiles_m) {
-  using T = Tile<FM>;
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  half_t* lds = reinterpret_cast<half_t*>(lds_raw);
-  __shared__ int last_flag;
+  extern __shared__ __align__(16) unsigned char lds[];
 
   // XCD-aware remap of the dispatch order, then M-fastest tile order.
   const int groups = gridDim.x;
@@ -198,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
   const int tile_n = rest / p.splits;
   const int tile = tile_n * tiles_m + tile_m;
 
-  const int m0 = tile_m * T::kBM;
+  const int m0 = tile_m * kBM;
   const int n0 = tile_n * kBN;
   const int k_per = p.k / p.splits;
   const int k_begin = split * k_per;
@@ -207,163 +243,166 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int group = wave >> 2;         // K substeps 2 group, 2 group + 1
+  const int wave_m = (wave >> 1) & 1;  // 64-row half of the tile
+  const int wave_n = wave & 1;         // 64-column half
 
-  half8 ra[T::kAChunks], rb[T::kBChunks];
-  auto load = [&](int kt) {
-    const int kk = k_begin + kt * kBK;
+  // DMA sources: wave w fills 1 KB blocks w * kAInstr + i of A (8 rows each)
+  // and of B; lane l brings row 8 b + l / 8 at LDS position l % 8, i.e.
+  // chunk Swizzle(row, l % 8). Rows past M or N read the last valid row
+  // (their results are never stored).
+  const half_t* a_src[kAInstr];
+  const half_t* b_src[kBInstr];
 #pragma unroll
-    for (int i = 0; i < T::kAChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c >> 3, c8 = (c & 7) * 8;
-      ra[i] = LoadChunk(p.x + static_cast<size_t>(m0 + row) * p.lda + kk + c8,
-                        m0 + row < p.m);
-    }
+  for (int i = 0; i < kAInstr; ++i) {
+    const int row = (wave * kAInstr + i) * 8 + (lane >> 3);
+    a_src[i] = p.x + static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda +
+               k_begin + Swizzle(row, lane & 7) * 8;
+  }
 #pragma unroll
-    for (int i = 0; i < T::kBChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c >> 3, c8 = (c & 7) * 8;
-      rb[i] = LoadChunk(p.w + static_cast<size_t>(n0 + row) * p.ldb + kk + c8,
-                        n0 + row < p.n);
-    }
-  };
-  auto store = [&](int buffer) {
-    half_t* as = lds + buffer * T::kStageHalves;
-    half_t* bs = as + T::kBM * kPitch;
+  for (int i = 0; i < kBInstr; ++i) {
+    const int row = (wave * kBInstr + i) * 8 + (lane >> 3);
+    b_src[i] = p.w + static_cast<size_t>(min(n0 + row, p.n - 1)) * p.ldb +
+               k_begin + Swizzle(row, lane & 7) * 8;
+  }
+  const uint32_t lds_base = LdsAddress(lds);
+  auto issue = [&](int stage, int kt) {
+    const uint32_t base = lds_base + stage * kStageBytes;
+    const int kk = kt * kBK;
 #pragma unroll
-    for (int i = 0; i < T::kAChunks; ++i) {
-      const int c = tid + i * kThreads;
-      *reinterpret_cast<half8*>(as + (c >> 3) * kPitch + (c & 7) * 8) = ra[i];
-    }
+    for (int i = 0; i < kAInstr; ++i)
+      DmaToLds(a_src[i] + kk, base + (wave * kAInstr + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < T::kBChunks; ++i) {
-      const int c = tid + i * kThreads;
-      *reinterpret_cast<half8*>(bs + (c >> 3) * kPitch + (c & 7) * 8) = rb[i];
-    }
+    for (int i = 0; i < kBInstr; ++i)
+      DmaToLds(b_src[i] + kk, base + kABytes + (wave * kBInstr + i) * 1024);
   };
 
-  floatx16 acc[FM][4];
+  floatx16 acc[2][2];
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm)
+  for (int fm = 0; fm < 2; ++fm)
 #pragma unroll
-    for (int fn = 0; fn < 4; ++fn)
+    for (int fn = 0; fn < 2; ++fn)
       acc[fm][fn] = floatx16{};
 
-  load(0);
-  store(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < steps)
+      issue(s, s);
   for (int kt = 0; kt < steps; ++kt) {
-    const int buffer = kt & 1;
-    if (kt + 1 < steps)
-      load(kt + 1);
-    const half_t* as = lds + buffer * T::kStageHalves;
-    const half_t* bs = as + T::kBM * kPitch;
+    // Stage kt has landed once at most `ahead` later stages are in flight.
+    const int ahead = min(STAGES - 2, steps - 1 - kt);
+    if (ahead >= 2)
+      WaitLoads<2 * kLoads>();
+    else if (ahead == 1)
+      WaitLoads<kLoads>();
+    else
+      WaitLoads<0>();
+    StageBarrier();
+    // Every wave is past its reads of stage kt - 1: refill that buffer.
+    if (kt + STAGES - 1 < steps)
+      issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+    const unsigned char* as = lds + (kt % STAGES) * kStageBytes;
+    const unsigned char* bs = as + kABytes;
+    half8 a[2][2], b[2][2];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int k_off = ks * 16 + (lane >> 5) * 8;
-      half8 a[FM], b[4];
+    for (int j = 0; j < 2; ++j) {
+      const int chunk = 2 * (2 * group + j) + (lane >> 5);
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-        a[fm] = *reinterpret_cast<const half8*>(
-            as + (wave * FM * 32 + fm * 32 + (lane & 31)) * kPitch + k_off);
-#pragma unroll
-      for (int fn = 0; fn < 4; ++fn)
-        b[fn] = *reinterpret_cast<const half8*>(
-            bs + (fn * 32 + (lane & 31)) * kPitch + k_off);
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < 4; ++fn)
-          acc[fm][fn] = Mfma32(a[fm], b[fn], acc[fm][fn]);
+      for (int f = 0; f < 2; ++f) {
+        const int ra = wave_m * 64 + f * 32 + (lane & 31);
+        a[j][f] = *reinterpret_cast<const half8*>(as + ra * 128 +
+                                                  Swizzle(ra, chunk) * 16);
+        const int rb = wave_n * 64 + f * 32 + (lane & 31);
+        b[j][f] = *reinterpret_cast<const half8*>(bs + rb * 128 +
+                                                  Swizzle(rb, chunk) * 16);
+      }
     }
-    if (kt + 1 < steps)
-      store(buffer ^ 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < 2; ++fn)
+          acc[fm][fn] = Mfma32(a[j][fm], b[j][fn], acc[fm][fn]);
+  }
+
+  // Sum the groups into the fp32 tile: group 1 stores, group 0 adds its own
+  // accumulators to what group 1 left (group 0 + group 1).
+  __syncthreads();
+  float* tile_lds = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int phase = 1; phase >= 0; --phase) {
+    if (group == phase) {
+#pragma unroll
+      for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < 2; ++fn)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wave_m * 64 + fm * 32 + 8 * (r / 4) +
+                            4 * (lane >> 5) + (r & 3);
+            const int col = wave_n * 64 + fn * 32 + (lane & 31);
+            float* cell = tile_lds + row * kPitch + col;
+            *cell = phase == 1 ? acc[fm][fn][r] : acc[fm][fn][r] + *cell;
+          }
+    }
     __syncthreads();
   }
 
   if (p.splits > 1) {
-    // Partial tile in accumulator order: float4 q of accumulator (fm, fn)
-    // of lane l at ((((wave * FM + fm) * 4 + fn) * 4 + q) * 64 + l) * 4.
-    float* mine = p.partials + (static_cast<size_t>(tile) * p.splits + split) *
-                                   T::kTileFloats;
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < 4; ++fn)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const floatx4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1],
-                             acc[fm][fn][4 * q + 2], acc[fm][fn][4 * q + 3]};
-          *reinterpret_cast<floatx4*>(
-              mine + ((((wave * FM + fm) * 4 + fn) * 4 + q) * 64 + lane) * 4) = v;
-        }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const int arrived = atomicAdd(p.counters + tile, 1);
-      last_flag = arrived == p.splits - 1;
+    float* mine = p.partials +
+                  (static_cast<size_t>(tile) * p.splits + split) * kTileFloats;
+    for (int f = tid; f < kTileFloats / 4; f += kThreads) {
+      const int row = f >> 5, c4 = (f & 31) * 4;
+      *reinterpret_cast<floatx4*>(mine + row * kBN + c4) =
+          *reinterpret_cast<const floatx4*>(tile_lds + row * kPitch + c4);
     }
-    __syncthreads();
-    if (!last_flag)
-      return;
-    __threadfence();
-    const float* base =
-        p.partials + static_cast<size_t>(tile) * p.splits * T::kTileFloats;
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < 4; ++fn)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const size_t off =
-              ((((wave * FM + fm) * 4 + fn) * 4 + q) * 64 + lane) * 4;
-          floatx4 sum = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1],
-                         acc[fm][fn][4 * q + 2], acc[fm][fn][4 * q + 3]};
-          if (split != 0)
-            sum = *reinterpret_cast<const floatx4*>(base + off);
-          for (int s = 1; s < p.splits; ++s) {
-            floatx4 v;
-            if (s == split)
-              v = floatx4{acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1],
-                          acc[fm][fn][4 * q + 2], acc[fm][fn][4 * q + 3]};
-            else
-              v = *reinterpret_cast<const floatx4*>(
-                  base + static_cast<size_t>(s) * T::kTileFloats + off);
-            sum += v;
-          }
-          acc[fm][fn][4 * q] = sum[0];
-          acc[fm][fn][4 * q + 1] = sum[1];
-          acc[fm][fn][4 * q + 2] = sum[2];
-          acc[fm][fn][4 * q + 3] = sum[3];
-        }
-    if (tid == 0)
-      p.counters[tile] = 0;
+    return;
   }
-
-  if constexpr (EPI == Epilogue::kStore)
-    Epilogue32<FM>(p, acc, m0, n0, false);
-  else if constexpr (EPI == Epilogue::kAccumulate)
-    Epilogue32<FM>(p, acc, m0, n0, true);
-  else if constexpr (EPI == Epilogue::kQkvRope)
-    EpilogueQkv<FM>(p, acc, m0, tile_n);
-  else
-    EpilogueSwiGlu<FM>(p, acc, m0, tile_n);
+  TileEpilogue<EPI>(p, tile_lds, tile_m, tile_n);
 }
 
-template <int FM, Epilogue EPI>
-void Launch(const GemmParams& p, int tiles_m, int groups,
-            hipStream_t stream) {
-  hipLaunchKernelGGL((GemmKernel<FM, EPI>), dim3(groups), dim3(kThreads),
-                     Tile<FM>::kLdsBytes, stream, p, tiles_m);
+// Sums a tile's split-K partials in split order 0, 1, ... (a fixed order,
+// reproducible bit for bit) into the LDS tile and applies the epilogue.
+template <Epilogue EPI>
+__global__ __launch_bounds__(kThreads) void SplitReduceKernel(GemmParams p,
+                                                              int tiles_m) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  float* tile_lds = reinterpret_cast<float*>(lds);
+  const int tile = blockIdx.x;
+  const float* base =
+      p.partials + static_cast<size_t>(tile) * p.splits * kTileFloats;
+  for (int f = threadIdx.x; f < kTileFloats / 4; f += kThreads) {
+    const int row = f >> 5, c4 = (f & 31) * 4;
+    floatx4 sum = *reinterpret_cast<const floatx4*>(base + row * kBN + c4);
+    for (int s = 1; s < p.splits; ++s)
+      sum += *reinterpret_cast<const floatx4*>(
+          base + static_cast<size_t>(s) * kTileFloats + row * kBN + c4);
+    *reinterpret_cast<floatx4*>(tile_lds + row * kPitch + c4) = sum;
+  }
+  __syncthreads();
+  TileEpilogue<EPI>(p, tile_lds, tile % tiles_m, tile / tiles_m);
+}
+
+template <int STAGES, Epilogue EPI>
+void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
+  GemmKernel<STAGES, EPI>
+      <<<dim3(groups), dim3(kThreads), LdsBytes<STAGES>(), stream>>>(p, tiles_m);
+  if (p.splits > 1)
+    SplitReduceKernel<EPI><<<dim3(groups / p.splits), dim3(kThreads),
+                             kEpilogueBytes, stream>>>(p, tiles_m);
 }
 
 template <Epilogue EPI>
 void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
-  const int tiles_m = (p.m + plan.block_m - 1) / plan.block_m;
+  const int tiles_m = (p.m + kBM - 1) / kBM;
   const int groups = plan.tiles * plan.splits;
-  if (plan.block_m == 256)
+  if (plan.stages == 2)
     Launch<2, EPI>(p, tiles_m, groups, stream);
+  else if (plan.stages == 4)
+    Launch<4, EPI>(p, tiles_m, groups, stream);
   else
-    Launch<1, EPI>(p, tiles_m, groups, stream);
+    Launch<3, EPI>(p, tiles_m, groups, stream);
 }
 
 }  // namespace
@@ -371,24 +410,25 @@ void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   (void)epilogue;
   GemmPlan plan;
-  plan.block_m = 128;
-  const int tiles_m = (m + plan.block_m - 1) / plan.block_m;
+  const int tiles_m = (m + kBM - 1) / kBM;
   const int tiles_n = (n + kBN - 1) / kBN;
   plan.tiles = tiles_m * tiles_n;
+  plan.stages = 3;
   const int k_steps = k / kBK;
-  // Split K until the grid covers the 256 CUs, keeping >= 2 K steps per
-  // split so the double buffer has something to overlap.
+  // Split K only when the tiles leave most CUs idle; partials cost a round
+  // trip through memory and a second launch.
   int splits = 1;
-  for (const int s : {2, 3, 4, 6, 8, 12, 16}) {
-    if (plan.tiles * splits >= 256)
-      break;
-    if (k_steps % s == 0 && k_steps / s >= 2)
-      splits = s;
+  if (plan.tiles < 64) {
+    for (const int s : {2, 3, 4, 6, 8}) {
+      if (plan.tiles * splits >= 128)
+        break;
+      if (k_steps % s == 0 && k_steps / s >= 4)
+        splits = s;
+    }
   }
   plan.splits = splits;
   plan.partial_floats =
-      splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits *
-                       plan.block_m * kBN
+      splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits * kTileFloats
                  : 0;
   return plan;
 }
@@ -399,9 +439,13 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
   Require(p.k % kBK == 0, "gemm: K must be a multiple of 64");
   Require(plan.splits >= 1 && (p.k / kBK) % plan.splits == 0,
           "gemm: K steps not divisible by the split count");
-  Require(p.lda % 8 == 0 && p.ldb % 8 == 0, "gemm: leading dimensions must be multiples of 8");
-  Require(plan.splits == 1 || (p.partials != nullptr && p.counters != nullptr),
-          "gemm: split-K needs partials and counters");
+  Require(plan.stages >= 2 && plan.stages <= 4, "gemm: 2 to 4 stages");
+  Require(plan.tiles == ((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN),
+          "gemm: plan does not match the shape");
+  Require(p.lda % 8 == 0 && p.ldb % 8 == 0,
+          "gemm: leading dimensions must be multiples of 8");
+  Require(plan.splits == 1 || p.partials != nullptr,
+          "gemm: split-K needs a partials buffer");
   Require(p.splits == plan.splits, "gemm: params and plan disagree on splits");
   switch (epilogue) {
     case Epilogue::kStore:
@@ -413,6 +457,7 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
     case Epilogue::kQkvRope:
       Require(p.n == (p.heads + 2 * p.kv_heads) * 128,
               "gemm: q/k/v epilogue needs N = (heads + 2 kv_heads) * 128");
+      Require(p.ldvt % 4 == 0, "gemm: V^T rows must be 8-byte aligned");
       LaunchEpi<Epilogue::kQkvRope>(p, plan, stream);
       break;
     case Epilogue::kSwiGlu:

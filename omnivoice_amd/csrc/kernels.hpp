@@ -49,7 +49,6 @@ struct GemmParams {
   int m, n, k;
   int splits;        // K split into `splits` equal ranges (1 = none)
   float* partials;   // [tiles * splits][tile floats] when splits > 1
-  int* counters;     // [tiles], zero between launches
   // kStore / kAccumulate
   float* y;
   int ldc;
@@ -69,10 +68,10 @@ struct GemmParams {
   int ldh;
 };
 
-// Picks the tile shape and split count for (m, n, k); returns the number
-// of floats of `partials` and ints of `counters` the launch needs.
+// Picks the tile shape and split count for (m, n, k) and the number of
+// floats of `partials` the launch needs.
 struct GemmPlan {
-  int block_m = 128;
+  int stages = 3;  // LDS ring depth: 2..4
   int splits = 1;
   int tiles = 0;
   std::size_t partial_floats = 0;

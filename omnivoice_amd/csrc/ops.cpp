@@ -141,10 +141,6 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
     const ovg::GemmPlan plan = ovg::PlanGemm(
         static_cast<int>(rows), static_cast<int>(out), static_cast<int>(in), epi);
     Scratch<float> partials(plan.partial_floats);
-    Scratch<int> counters(static_cast<std::size_t>(plan.tiles));
-    ovg::Check(hipMemsetAsync(counters.data, 0,
-                              static_cast<std::size_t>(plan.tiles) * sizeof(int), s),
-               "clear counters");
     ovg::GemmParams p{};
     p.x = static_cast<const ovg::half_t*>(x);
     p.w = static_cast<const ovg::half_t*>(w);
@@ -155,7 +151,6 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
     p.k = static_cast<int>(in);
     p.splits = plan.splits;
     p.partials = partials.data;
-    p.counters = counters.data;
     p.y = y;
     p.ldc = static_cast<int>(out);
     ovg::LaunchGemm(p, plan, epi, s);

@@ -267,7 +267,7 @@ class Engine {
   DeviceBuffer<SelectItem> select_items_;
   DeviceBuffer<float> hidden_, logits_, conf_, noise_, partials_;
   DeviceBuffer<half_t> normed_, qk_, vt_, attn_, act_, final_normed_;
-  DeviceBuffer<int> pred_, codes_, unmasked_at_, counters_;
+  DeviceBuffer<int> pred_, codes_, unmasked_at_;
   DeviceBuffer<SelectStep> plan_;
 
   std::map<std::string, std::unique_ptr<GraphEntry>> graphs_;
@@ -503,7 +503,7 @@ std::int64_t Engine::DeviceBytes() const {
            partials_.bytes() + normed_.bytes() + qk_.bytes() + vt_.bytes() +
            attn_.bytes() + act_.bytes() + final_normed_.bytes() +
            pred_.bytes() + codes_.bytes() + unmasked_at_.bytes() +
-           counters_.bytes() + plan_.bytes();
+           plan_.bytes();
   return static_cast<std::int64_t>(total);
 }
 
@@ -639,7 +639,7 @@ void Engine::Prepare(const Layout& L) {
   Grow(conf_, static_cast<std::size_t>(L.outputs));
   Grow(codes_, static_cast<std::size_t>(L.outputs));
   Grow(unmasked_at_, static_cast<std::size_t>(L.outputs));
-  std::size_t partials = 0, counters = 0;
+  std::size_t partials = 0;
   const int M = L.rows;
   const int K = static_cast<int>(cfg_.hidden_size);
   for (const auto& [m, n, k] : {
@@ -650,10 +650,8 @@ void Engine::Prepare(const Layout& L) {
            {L.targets, static_cast<int>(width), K}}) {
     const GemmPlan plan = PlanGemm(m, n, k, Epilogue::kStore);
     partials = std::max(partials, plan.partial_floats);
-    counters = std::max(counters, static_cast<std::size_t>(plan.tiles));
   }
   Grow(partials_, std::max<std::size_t>(partials, 1));
-  Grow(counters_, std::max<std::size_t>(counters, 1));
   auto up = [&](void* dst, const void* src, std::size_t bytes) {
     Check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_),
           "upload batch");
@@ -719,7 +717,6 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     p.k = k;
     p.splits = plan.splits;
     p.partials = partials_.get();
-    p.counters = counters_.get();
     set(p);
     const double flops = 2.0 * real_m * n * k;
     const double bytes = 2.0 * n * k + 2.0 * real_m * k + out_bytes;

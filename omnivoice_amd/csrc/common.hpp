@@ -29,6 +29,31 @@ __device__ __forceinline__ float WaveSum(float v) {
   return v;
 }
 
+// Wave sum without LDS traffic: DPP within 16-lane rows (swap neighbours,
+// swap pairs, half-row mirror, row mirror), then the four row sums read with
+// v_readlane and added as (row 0 + row 1) + (row 2 + row 3). Every lane gets
+// the total. Its summation tree differs from WaveSum's, so the bit-exact
+// score uses WaveSum.
+template <int CTRL>
+__device__ __forceinline__ float DppAdd(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                CTRL, 0xF, 0xF, false);
+  return v + __builtin_bit_cast(float, moved);
+}
+
+__device__ __forceinline__ float WaveSumFast(float v) {
+  v = DppAdd<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = DppAdd<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = DppAdd<0x141>(v);  // row_half_mirror
+  v = DppAdd<0x140>(v);  // row_mirror
+  const int bits = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float WaveMax(float v) {
   for (int offset = kWave / 2; offset > 0; offset /= 2)
     v = fmaxf(v, __shfl_xor(v, offset));

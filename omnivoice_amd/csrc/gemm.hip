@@ -145,20 +145,31 @@ __device__ __forceinline__ void QkvRows(const GemmParams& p, const float* tile,
   if (slot < p.heads + p.kv_heads) {
     const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
     const float w0 = weight[lane], w1 = weight[lane + 64];
-    for (int r = wave; r < kBM; r += kThreads / 64) {
+    // The wave's rows are wave + 8 i; fetch their positions (lane i holds
+    // row i's) and all rotary entries before the row loop, so the loads'
+    // latency is paid once rather than per row.
+    constexpr int kRows = kBM / (kThreads / 64);
+    const int my_row = min(m0 + wave + 8 * (lane & (kRows - 1)), p.m - 1);
+    const int positions = p.positions[my_row];
+    float2 cs[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+      cs[i] = p.rope[static_cast<size_t>(__shfl(positions, i)) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int r = wave + 8 * i;
       const int m = m0 + r;
       if (m >= p.m)
         break;
       const float v0 = tile[r * kPitch + lane];
       const float v1 = tile[r * kPitch + lane + 64];
-      const float squares = WaveSum(v0 * v0 + v1 * v1);
+      const float squares = WaveSumFast(v0 * v0 + v1 * v1);
       const float scale = rsqrtf(squares * (1.0F / 128.0F) + p.eps);
-      const float2 cs = p.rope[static_cast<size_t>(p.positions[m]) * 64 + lane];
       const float a = w0 * (v0 * scale);
       const float b = w1 * (v1 * scale);
       half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
-      out[lane] = static_cast<half_t>(a * cs.x - b * cs.y);
-      out[lane + 64] = static_cast<half_t>(b * cs.x + a * cs.y);
+      out[lane] = static_cast<half_t>(a * cs[i].x - b * cs[i].y);
+      out[lane + 64] = static_cast<half_t>(b * cs[i].x + a * cs[i].y);
     }
     return;
   }
@@ -204,7 +215,7 @@ __device__ __forceinline__ void TileEpilogue(const GemmParams& p,
                                              const float* tile, int tile_m,
                                              int tile_n) {
   const int m0 = tile_m * kBM;
-  if constexpr (EPI == Epilogue::kStore)
+  if constexpr (EPI == Epilogue::kStore || EPI == Epilogue::kPartial)
     StoreRows(p, tile, m0, tile_n * kBN, false);
   else if constexpr (EPI == Epilogue::kAccumulate)
     StoreRows(p, tile, m0, tile_n * kBN, true);
@@ -349,6 +360,14 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     __syncthreads();
   }
 
+  if constexpr (EPI == Epilogue::kPartial) {
+    // Each split owns a full [M][ldc] slice; the row kernel that consumes
+    // the GEMM adds the slices.
+    GemmParams q = p;
+    q.y = p.y + static_cast<size_t>(split) * p.split_stride;
+    TileEpilogue<EPI>(q, tile_lds, tile_m, tile_n);
+    return;
+  }
   if (p.splits > 1) {
     float* mine = p.partials +
                   (static_cast<size_t>(tile) * p.splits + split) * kTileFloats;
@@ -388,7 +407,7 @@ template <int STAGES, Epilogue EPI>
 void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
   GemmKernel<STAGES, EPI>
       <<<dim3(groups), dim3(kThreads), LdsBytes<STAGES>(), stream>>>(p, tiles_m);
-  if (p.splits > 1)
+  if (p.splits > 1 && EPI != Epilogue::kPartial)
     SplitReduceKernel<EPI><<<dim3(groups / p.splits), dim3(kThreads),
                              kEpilogueBytes, stream>>>(p, tiles_m);
 }
@@ -408,16 +427,29 @@ void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
 }  // namespace
 
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
-  (void)epilogue;
   GemmPlan plan;
   const int tiles_m = (m + kBM - 1) / kBM;
   const int tiles_n = (n + kBN - 1) / kBN;
   plan.tiles = tiles_m * tiles_n;
   plan.stages = 3;
   const int k_steps = k / kBK;
-  // Split K only when the tiles leave most CUs idle; partials cost a round
-  // trip through memory and a second launch.
   int splits = 1;
+  if (epilogue == Epilogue::kPartial) {
+    // Split slices are summed by the row kernel that reads the output
+    // anyway: split until the grid covers most CUs, keeping >= 8 K steps
+    // per split for the DMA ring to overlap.
+    for (const int s : {2, 3, 4, 6, 8}) {
+      if (plan.tiles * splits >= 160)
+        break;
+      if (k_steps % s == 0 && k_steps / s >= 8)
+        splits = s;
+    }
+    plan.splits = splits;
+    plan.partial_floats = 0;
+    return plan;
+  }
+  // Otherwise split K only when the tiles leave most CUs idle; partials
+  // cost a round trip through memory and a second launch.
   if (plan.tiles < 64) {
     for (const int s : {2, 3, 4, 6, 8}) {
       if (plan.tiles * splits >= 128)
@@ -444,7 +476,8 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
           "gemm: plan does not match the shape");
   Require(p.lda % 8 == 0 && p.ldb % 8 == 0,
           "gemm: leading dimensions must be multiples of 8");
-  Require(plan.splits == 1 || p.partials != nullptr,
+  Require(plan.splits == 1 || epilogue == Epilogue::kPartial ||
+              p.partials != nullptr,
           "gemm: split-K needs a partials buffer");
   Require(p.splits == plan.splits, "gemm: params and plan disagree on splits");
   switch (epilogue) {
@@ -463,6 +496,12 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
     case Epilogue::kSwiGlu:
       Require(p.n % 128 == 0, "gemm: SwiGLU epilogue needs N % 128 == 0");
       LaunchEpi<Epilogue::kSwiGlu>(p, plan, stream);
+      break;
+    case Epilogue::kPartial:
+      Require(p.y != nullptr &&
+                  p.split_stride >= static_cast<std::size_t>(p.m) * p.ldc,
+              "gemm: partial slices overlap");
+      LaunchEpi<Epilogue::kPartial>(p, plan, stream);
       break;
   }
   Check(hipGetLastError(), "gemm launch");

@@ -40,6 +40,8 @@ enum class Epilogue : int {
   kSwiGlu = 3,      // W rows interleaved per 128-row tile as 64 gate rows
                     // then the matching 64 up rows; act fp16 [M][ldh] =
                     // silu(gate) * up
+  kPartial = 4,     // split s stores its fp32 tile to y + s * split_stride
+                    // ([M][ldc] per split); a row kernel sums the splits
 };
 
 struct GemmParams {
@@ -49,6 +51,7 @@ struct GemmParams {
   int m, n, k;
   int splits;        // K split into `splits` equal ranges (1 = none)
   float* partials;   // [tiles * splits][tile floats] when splits > 1
+  std::size_t split_stride;  // kPartial: floats between split slices of y
   // kStore / kAccumulate
   float* y;
   int ldc;
@@ -101,6 +104,25 @@ void LaunchEmbed(const EmbedParams& p, hipStream_t stream);
 void LaunchRmsNorm(const float* x, const int* gather, const float* w,
                    half_t* out, int rows, int width, float eps,
                    hipStream_t stream);
+
+// The residual update and the next RMSNorm in one pass over rows:
+//   h = hidden[src] + partial[0][src] + partial[1][src] + ... (that order)
+//   out[r] = half(norm * h * rsqrt(mean(h^2) + eps))
+// With `gather` null, src = r and h is written back to hidden[r]; with
+// `gather` set, src = gather[r] and hidden is left untouched (the final
+// norm of the target rows).
+struct AddNormParams {
+  float* hidden;             // [rows][width]
+  const float* partials;     // splits slices of [rows][width]
+  std::size_t split_stride;  // floats between slices
+  int splits;
+  const float* norm;         // [width]
+  half_t* out;               // [rows][width]
+  const int* gather;
+  int rows, width;
+  float eps;
+};
+void LaunchAddNorm(const AddNormParams& p, hipStream_t stream);
 
 // vt[g][d][ldvt] = qkv[r][(heads + kv_heads + g) * 128 + d] for r < rows.
 void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,

@@ -14,7 +14,7 @@ namespace {
 constexpr int kRowThreads = 256;
 
 __device__ __forceinline__ float BlockSum(float v, float* scratch) {
-  v = WaveSum(v);
+  v = WaveSumFast(v);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0)
     scratch[wave] = v;
@@ -79,40 +79,103 @@ __global__ __launch_bounds__(kRowThreads) void EmbedKernel(EmbedParams p) {
   }
 }
 
+// One wave per row, four rows per work-group: lane l owns the float4
+// columns 4 (l + 64 i), so every load is a contiguous 1 KB per wave and the
+// row sum of squares is one wave butterfly (no barriers). CHUNKS float4 per
+// lane cover widths up to 256 CHUNKS.
+template <int CHUNKS>
 __global__ __launch_bounds__(kRowThreads) void RmsNormKernel(
-    const float* x, const int* gather, const float* w, half_t* out, int width,
-    float eps) {
-  __shared__ float scratch[4];
-  const int row = blockIdx.x;
-  const int src = gather != nullptr ? gather[row] : row;
+    const float* x, const int* gather, const float* w, half_t* out, int rows,
+    int width, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  if (r >= rows)
+    return;
+  const int src = gather != nullptr ? gather[r] : r;
   const float* in = x + static_cast<size_t>(src) * width;
-  constexpr int kMaxChunks = 4;
-  floatx4 v[kMaxChunks];
+  floatx4 v[CHUNKS];
   float squares = 0.0F;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const int d = (threadIdx.x + i * kRowThreads) * 4;
-    v[i] = floatx4{0, 0, 0, 0};
-    if (d < width) {
-      v[i] = *reinterpret_cast<const floatx4*>(in + d);
-      squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
-                 v[i][3] * v[i][3];
+  for (int i = 0; i < CHUNKS; ++i) {
+    const int d = (lane + 64 * i) * 4;
+    v[i] = d < width ? *reinterpret_cast<const floatx4*>(in + d)
+                     : floatx4{0, 0, 0, 0};
+    squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
+               v[i][3] * v[i][3];
+  }
+  const float scale = rsqrtf(WaveSumFast(squares) / static_cast<float>(width) + eps);
+  half_t* o = out + static_cast<size_t>(r) * width;
+#pragma unroll
+  for (int i = 0; i < CHUNKS; ++i) {
+    const int d = (lane + 64 * i) * 4;
+    if (d >= width)
+      break;
+    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + d);
+    *reinterpret_cast<half4*>(o + d) =
+        half4{static_cast<half_t>(wv[0] * (v[i][0] * scale)),
+              static_cast<half_t>(wv[1] * (v[i][1] * scale)),
+              static_cast<half_t>(wv[2] * (v[i][2] * scale)),
+              static_cast<half_t>(wv[3] * (v[i][3] * scale))};
+  }
+}
+
+// Residual update + RMSNorm (see AddNormParams), one wave per row. All of a
+// row's loads (hidden and every split slice) are issued before the sum, which
+// then runs in the fixed order hidden + slice 0 + slice 1 + ...
+template <int CHUNKS, int MAX_SPLITS>
+__global__ __launch_bounds__(kRowThreads) void AddNormKernel(AddNormParams p) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  if (r >= p.rows)
+    return;
+  const int src = p.gather != nullptr ? p.gather[r] : r;
+  float* h = p.hidden + static_cast<size_t>(src) * p.width;
+  const float* part = p.partials + static_cast<size_t>(src) * p.width;
+  floatx4 v[CHUNKS];
+  floatx4 parts[MAX_SPLITS][CHUNKS];
+#pragma unroll
+  for (int i = 0; i < CHUNKS; ++i) {
+    const int d = (lane + 64 * i) * 4;
+    const bool ok = d < p.width;
+    v[i] = ok ? *reinterpret_cast<const floatx4*>(h + d) : floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; ++s)
+      parts[s][i] = ok && s < p.splits
+                        ? *reinterpret_cast<const floatx4*>(part + s * p.split_stride + d)
+                        : floatx4{0, 0, 0, 0};
+  }
+  float squares = 0.0F;
+#pragma unroll
+  for (int i = 0; i < CHUNKS; ++i) {
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; ++s)
+      if (s < p.splits)
+        v[i] += parts[s][i];
+    squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
+               v[i][3] * v[i][3];
+  }
+  if (p.gather == nullptr) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int d = (lane + 64 * i) * 4;
+      if (d < p.width)
+        *reinterpret_cast<floatx4*>(h + d) = v[i];
     }
   }
-  const float total = BlockSum(squares, scratch);
-  const float scale = rsqrtf(total / static_cast<float>(width) + eps);
-  half_t* o = out + static_cast<size_t>(row) * width;
+  const float scale =
+      rsqrtf(WaveSumFast(squares) / static_cast<float>(p.width) + p.eps);
+  half_t* o = p.out + static_cast<size_t>(r) * p.width;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const int d = (threadIdx.x + i * kRowThreads) * 4;
-    if (d >= width)
-      continue;
-    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + d);
-    const half4 h = {static_cast<half_t>(wv[0] * (v[i][0] * scale)),
-                     static_cast<half_t>(wv[1] * (v[i][1] * scale)),
-                     static_cast<half_t>(wv[2] * (v[i][2] * scale)),
-                     static_cast<half_t>(wv[3] * (v[i][3] * scale))};
-    *reinterpret_cast<half4*>(o + d) = h;
+  for (int i = 0; i < CHUNKS; ++i) {
+    const int d = (lane + 64 * i) * 4;
+    if (d >= p.width)
+      break;
+    const floatx4 wv = *reinterpret_cast<const floatx4*>(p.norm + d);
+    *reinterpret_cast<half4*>(o + d) =
+        half4{static_cast<half_t>(wv[0] * (v[i][0] * scale)),
+              static_cast<half_t>(wv[1] * (v[i][1] * scale)),
+              static_cast<half_t>(wv[2] * (v[i][2] * scale)),
+              static_cast<half_t>(wv[3] * (v[i][3] * scale))};
   }
 }
 
@@ -149,11 +212,29 @@ void LaunchRmsNorm(const float* x, const int* gather, const float* w,
                    half_t* out, int rows, int width, float eps,
                    hipStream_t stream) {
   Require(rows > 0, "rmsnorm: no rows");
-  Require(width % 4 == 0 && width <= 4 * 4 * kRowThreads,
+  Require(width % 4 == 0 && width <= 4096,
           "rmsnorm: width must be a multiple of 4 and at most 4096");
-  hipLaunchKernelGGL(RmsNormKernel, dim3(rows), dim3(kRowThreads), 0, stream,
-                     x, gather, w, out, width, eps);
+  const dim3 grid((rows + kRowThreads / 64 - 1) / (kRowThreads / 64));
+  if (width <= 1024)
+    RmsNormKernel<4><<<grid, kRowThreads, 0, stream>>>(x, gather, w, out, rows,
+                                                       width, eps);
+  else
+    RmsNormKernel<16><<<grid, kRowThreads, 0, stream>>>(x, gather, w, out,
+                                                        rows, width, eps);
   Check(hipGetLastError(), "rmsnorm launch");
+}
+
+void LaunchAddNorm(const AddNormParams& p, hipStream_t stream) {
+  Require(p.rows > 0, "addnorm: no rows");
+  Require(p.width % 4 == 0 && p.width <= 1024,
+          "addnorm: width must be a multiple of 4 and at most 1024");
+  Require(p.splits >= 1 && p.splits <= 8, "addnorm: 1 to 8 partial slices");
+  const dim3 grid((p.rows + kRowThreads / 64 - 1) / (kRowThreads / 64));
+  if (p.splits <= 4)
+    AddNormKernel<4, 4><<<grid, kRowThreads, 0, stream>>>(p);
+  else
+    AddNormKernel<4, 8><<<grid, kRowThreads, 0, stream>>>(p);
+  Check(hipGetLastError(), "addnorm launch");
 }
 
 void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,

@@ -265,7 +265,7 @@ class Engine {
   DeviceBuffer<AttentionWork> work_;
   DeviceBuffer<ScoreItem> score_items_;
   DeviceBuffer<SelectItem> select_items_;
-  DeviceBuffer<float> hidden_, logits_, conf_, noise_, partials_;
+  DeviceBuffer<float> hidden_, logits_, conf_, noise_, partials_, part_;
   DeviceBuffer<half_t> normed_, qk_, vt_, attn_, act_, final_normed_;
   DeviceBuffer<int> pred_, codes_, unmasked_at_;
   DeviceBuffer<SelectStep> plan_;
@@ -500,7 +500,8 @@ std::int64_t Engine::DeviceBytes() const {
            gather_.bytes() + epoch_.bytes() + work_.bytes() +
            score_items_.bytes() + select_items_.bytes() + hidden_.bytes() +
            logits_.bytes() + conf_.bytes() + noise_.bytes() +
-           partials_.bytes() + normed_.bytes() + qk_.bytes() + vt_.bytes() +
+           partials_.bytes() + part_.bytes() + normed_.bytes() + qk_.bytes() +
+           vt_.bytes() +
            attn_.bytes() + act_.bytes() + final_normed_.bytes() +
            pred_.bytes() + codes_.bytes() + unmasked_at_.bytes() +
            plan_.bytes();
@@ -644,14 +645,16 @@ void Engine::Prepare(const Layout& L) {
   const int K = static_cast<int>(cfg_.hidden_size);
   for (const auto& [m, n, k] : {
            std::tuple<int, int, int>{M, static_cast<int>(qk_width + cfg_.kv_heads * 128), K},
-           {M, K, static_cast<int>(cfg_.heads * 128)},
            {M, static_cast<int>(2 * cfg_.intermediate_size), K},
-           {M, K, static_cast<int>(cfg_.intermediate_size)},
            {L.targets, static_cast<int>(width), K}}) {
     const GemmPlan plan = PlanGemm(m, n, k, Epilogue::kStore);
     partials = std::max(partials, plan.partial_floats);
   }
   Grow(partials_, std::max<std::size_t>(partials, 1));
+  const int slices = std::max(
+      PlanGemm(M, K, static_cast<int>(cfg_.heads * 128), Epilogue::kPartial).splits,
+      PlanGemm(M, K, static_cast<int>(cfg_.intermediate_size), Epilogue::kPartial).splits);
+  Grow(part_, static_cast<std::size_t>(slices) * ra * h);
   auto up = [&](void* dst, const void* src, std::size_t bytes) {
     Check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_),
           "upload batch");
@@ -740,13 +743,31 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
                        (static_cast<double>(it.length) * it.length +
                         static_cast<double>(it.frames) * it.frames);
 
+  // The o and down projections leave their K-split slices in part_; the
+  // next row kernel adds them to the residual stream and applies the
+  // following RMSNorm (post-attention, the next layer's input norm, or the
+  // final norm on the target rows only).
+  const std::size_t part_stride = static_cast<std::size_t>(L.rows_alloc) * H;
+  auto add_norm = [&](const char* name, int splits, const float* norm,
+                      half_t* out, const int* gather, int rows) {
+    AddNormParams a{};
+    a.hidden = hidden_.get();
+    a.partials = part_.get();
+    a.split_stride = part_stride;
+    a.splits = splits;
+    a.norm = norm;
+    a.out = out;
+    a.gather = gather;
+    a.rows = rows;
+    a.width = H;
+    a.eps = cfg_.rms_norm_eps;
+    Run(prof, name, 0.0, static_cast<double>(rows) * H * (4.0 * (splits + 2) + 2.0),
+        [&] { LaunchAddNorm(a, stream_); });
+  };
+  const int o_splits = PlanGemm(M, H, heads_width, Epilogue::kPartial).splits;
+  const int down_splits = PlanGemm(M, H, I, Epilogue::kPartial).splits;
   for (std::size_t l = 0; l < layers_.size(); ++l) {
     const Layer& W = layers_[l];
-    if (l > 0)
-      Run(prof, "rmsnorm", 0.0, R * H * 6.0, [&] {
-        LaunchRmsNorm(hidden_.get(), nullptr, W.input_norm.get(),
-                      normed_.get(), M, H, cfg_.rms_norm_eps, stream_);
-      });
     gemm("gemm_qkv_rope", Epilogue::kQkvRope, normed_.get(), H, W.qkv.get(),
          M, qkv_n, H, R, R * qkv_n * 2.0, [&](GemmParams& p) {
            p.qk = qk_.get();
@@ -763,33 +784,32 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
          });
     Run(prof, "attention", attention_flops, R * (qkv_n + heads_width) * 2.0,
         [&] { LaunchAttention(ap, stream_); });
-    gemm("gemm_o_residual", Epilogue::kAccumulate, attn_.get(), heads_width,
-         W.output.get(), M, H, heads_width, R, R * H * 8.0,
+    gemm("gemm_o_partial", Epilogue::kPartial, attn_.get(), heads_width,
+         W.output.get(), M, H, heads_width, R, R * H * 4.0 * o_splits,
          [&](GemmParams& p) {
-           p.y = hidden_.get();
+           p.y = part_.get();
            p.ldc = H;
+           p.split_stride = part_stride;
          });
-    Run(prof, "rmsnorm", 0.0, R * H * 6.0, [&] {
-      LaunchRmsNorm(hidden_.get(), nullptr, W.post_norm.get(), normed_.get(),
-                    M, H, cfg_.rms_norm_eps, stream_);
-    });
+    add_norm("add_norm", o_splits, W.post_norm.get(), normed_.get(), nullptr, M);
     gemm("gemm_gate_up_swiglu", Epilogue::kSwiGlu, normed_.get(), H,
          W.gate_up.get(), M, 2 * I, H, R, R * I * 2.0, [&](GemmParams& p) {
            p.act = act_.get();
            p.ldh = I;
          });
-    gemm("gemm_down_residual", Epilogue::kAccumulate, act_.get(), I,
-         W.down.get(), M, H, I, R, R * H * 8.0, [&](GemmParams& p) {
-           p.y = hidden_.get();
+    gemm("gemm_down_partial", Epilogue::kPartial, act_.get(), I, W.down.get(),
+         M, H, I, R, R * H * 4.0 * down_splits, [&](GemmParams& p) {
+           p.y = part_.get();
            p.ldc = H;
+           p.split_stride = part_stride;
          });
+    if (l + 1 < layers_.size())
+      add_norm("add_norm", down_splits, layers_[l + 1].input_norm.get(),
+               normed_.get(), nullptr, M);
+    else  // GatherRows + final RmsNorm (generator.cpp:295-298)
+      add_norm("add_norm_final", down_splits, final_norm_.get(),
+               final_normed_.get(), gather_.get(), L.targets);
   }
-  // GatherRows + final RmsNorm, then the audio heads.
-  Run(prof, "final_norm", 0.0, L.targets * H * 6.0, [&] {
-    LaunchRmsNorm(hidden_.get(), gather_.get(), final_norm_.get(),
-                  final_normed_.get(), L.targets, H, cfg_.rms_norm_eps,
-                  stream_);
-  });
   gemm("gemm_audio_heads", Epilogue::kStore, final_normed_.get(), H,
        heads_.get(), L.targets, Vw, H, L.targets,
        static_cast<double>(L.targets) * Vw * 4.0, [&](GemmParams& p) {

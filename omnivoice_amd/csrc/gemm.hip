@@ -9,27 +9,32 @@
 //
 // One work-group computes a 128 x 128 output tile with 8 waves: two groups
 // of four split each 64-wide K step between them (substeps 0-1 and 2-3), and
-// inside a group the waves form a 2 x 2 grid of 64 x 64 sub-tiles. Two waves
-// per SIMD hide each other's LDS latency, and 64 x 64 wave tiles read 4 KB
-// of LDS per 4 MFMAs; gfx950's LDS delivers ~180 B/clk/CU with 8 waves but
-// only ~100 with 4, which is what bounded a 4-wave tile.
+// inside a group wave w owns the 32 x 128 strip of rows 32 w .. 32 w + 31.
+// A strip spans a whole 128-column tile, so one Qwen3 head (or one gate/up
+// block) lives in one wave and every epilogue works from registers. Two
+// waves per SIMD hide each other's LDS latency.
 //
 // Operands go global -> LDS by DMA (global_load_lds_dwordx4) through a
 // 2- to 4-stage ring of 32 KB stages, no registers involved; LDS rows are
-// 128 bytes with an XOR swizzle of the 16-byte chunks.
+// 128 bytes with an XOR swizzle of the 16-byte chunks. Fragments of step
+// k + 1 are read from LDS while step k's MFMAs run.
 //
-// Epilogue: the two groups' accumulators are summed into an fp32 tile in
-// LDS (group 0 + group 1, a fixed order), then all 8 waves walk the tile by
-// rows: plain or residual-accumulating fp32 stores; the q/k/v epilogue (a
-// Qwen3 head is one 128-column tile: per-head RMSNorm is one wave
-// reduction, rotate-half pairs are columns l and l + 64 of lane l, value
-// heads are written transposed); or SwiGLU over the interleaved gate/up
-// weight tile (columns l and l + 64 are the gate and up of one output).
+// Epilogue: the two groups swap halves of their accumulators through LDS
+// (16-byte per lane, conflict-free) so that each wave ends up owning 16 rows
+// x 128 columns of the summed tile (group 0 + group 1; fp32 addition of two
+// terms is commutative, so both owners round identically), and writes them
+// straight from registers: plain or residual-accumulating fp32 stores; the
+// q/k/v epilogue (per-head RMSNorm is a 32-lane reduction, rotate-half pairs
+// are columns c and c + 64 of the same lane, value heads are written
+// transposed, four consecutive rows per 8-byte store); or SwiGLU over the
+// interleaved gate/up weight tile (columns c and c + 64 are the gate and up
+// of one output).
 //
-// Split-K (for small M only): work-groups store their reduced tile as a
-// partial and a second launch sums the partials in split order 0, 1, ...
-// and runs the same epilogue; the kernel boundary publishes the partials to
-// every XCD.
+// Split-K: with the kPartial epilogue every split stores its own fp32 slice
+// and the row kernel that consumes the output sums the slices. Otherwise
+// (small M only) each split stores its owned values as a partial and a
+// second launch sums the partials in split order 0, 1, ... and runs the same
+// epilogue; the kernel boundary publishes the partials to every XCD.
 //
 // Work-groups are dispatched round-robin over the 8 XCDs; the block index is
 // remapped so that each XCD receives a contiguous run of tiles, ordered
@@ -50,14 +55,14 @@ constexpr int kStageBytes = kABytes + kBBytes;
 constexpr int kAInstr = kABytes / 1024 / 8;  // 1 KB DMA blocks per wave
 constexpr int kBInstr = kBBytes / 1024 / 8;
 constexpr int kLoads = kAInstr + kBInstr;  // DMA instructions per stage
-constexpr int kPitch = kBN + 4;            // floats per row of the fp32 tile
 constexpr int kTileFloats = kBM * kBN;
-constexpr int kEpilogueBytes = kBM * kPitch * 4;
+// The accumulator swap: each wave hands over 8 x 16 bytes per lane.
+constexpr int kSwapBytes = kThreads * 8 * 16;
 
 template <int STAGES>
 constexpr int LdsBytes() {
-  return STAGES * kStageBytes > kEpilogueBytes ? STAGES * kStageBytes
-                                               : kEpilogueBytes;
+  return STAGES * kStageBytes > kSwapBytes ? STAGES * kStageBytes
+                                           : kSwapBytes;
 }
 
 // LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
@@ -79,13 +84,17 @@ __device__ __forceinline__ int Swizzle(int row, int chunk) {
 // compiler's wait-count pass cannot tell which stage buffer such a load
 // writes and would wait for every load in flight before any LDS read, which
 // serialises the ring; the kernel waits explicitly instead.
-__device__ __forceinline__ void DmaToLds(const void* src, uint32_t lds_addr) {
+// The source is a wave-uniform base (scalar registers) plus a per-lane
+// 32-bit byte offset, so that advancing a K step is one scalar add and the
+// LDS address is scalar too: no vector work per DMA.
+__device__ __forceinline__ void DmaToLds(const unsigned char* base,
+                                         uint32_t offset, uint32_t lds_addr) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off"
+      "global_load_lds_dwordx4 %1, %2"
       :
-      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src)
+      : "s"(lds_addr), "v"(offset), "s"(base)
       : "memory", "m0");
 }
 
@@ -105,124 +114,143 @@ __device__ __forceinline__ void StageBarrier() {
 }
 
 // ------------------------------------------------------------- epilogues
-// All read the summed fp32 tile from LDS ([kBM][kPitch]) with 512 threads.
+// A wave's owned values: v[c][e] is column 32 c + (lane & 31) of row
+// row0 + RowOf(e), e < 8, where row0 = m0 + 32 wave_m + 16 group.
+struct Owned {
+  float v[4][8];
+};
 
-__device__ __forceinline__ void StoreRows(const GemmParams& p,
-                                          const float* tile, int m0, int n0,
-                                          bool accumulate) {
+__device__ __forceinline__ int RowOf(int e, int lane) {
+  return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+
+// Sum over the 32 lanes that share lane >> 5: DPP within 16-lane rows, then
+// the two rows of each half.
+__device__ __forceinline__ float HalfWaveSum(float v) {
+  v = DppAdd<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = DppAdd<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = DppAdd<0x141>(v);  // row_half_mirror
+  v = DppAdd<0x140>(v);  // row_mirror
+  return v + __shfl_xor(v, 16);
+}
+
+__device__ __forceinline__ void StoreOwned(const GemmParams& p, const Owned& o,
+                                           float* y, int row0, int n0,
+                                           bool accumulate) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int r = wave; r < kBM; r += kThreads / 64) {
-    const int m = m0 + r;
-    if (m >= p.m)
-      break;
-    const int n = n0 + 2 * lane;
-    const float2 v = *reinterpret_cast<const float2*>(tile + r * kPitch + 2 * lane);
-    float* dst = p.y + static_cast<size_t>(m) * p.ldc + n;
-    if (n + 1 < p.n && (p.ldc & 1) == 0) {
-      float2* d2 = reinterpret_cast<float2*>(dst);
-      if (accumulate) {
-        float2 o = *d2;
-        o.x += v.x;
-        o.y += v.y;
-        *d2 = o;
-      } else {
-        *d2 = v;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int n = n0 + 32 * c + (lane & 31);
+    if (n >= p.n)
+      continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int m = row0 + RowOf(e, lane);
+      if (m < p.m) {
+        float* dst = y + static_cast<size_t>(m) * p.ldc + n;
+        *dst = accumulate ? *dst + o.v[c][e] : o.v[c][e];
       }
-    } else {
-      if (n < p.n)
-        dst[0] = accumulate ? dst[0] + v.x : v.x;
-      if (n + 1 < p.n)
-        dst[1] = accumulate ? dst[1] + v.y : v.y;
     }
   }
 }
 
-__device__ __forceinline__ void QkvRows(const GemmParams& p, const float* tile,
-                                        int m0, int slot) {
+__device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
+                                         int row0, int slot) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int j = lane & 31;
   if (slot < p.heads + p.kv_heads) {
     const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
-    const float w0 = weight[lane], w1 = weight[lane + 64];
-    // The wave's rows are wave + 8 i; fetch their positions (lane i holds
-    // row i's) and all rotary entries before the row loop, so the loads'
-    // latency is paid once rather than per row.
-    constexpr int kRows = kBM / (kThreads / 64);
-    const int my_row = min(m0 + wave + 8 * (lane & (kRows - 1)), p.m - 1);
-    const int positions = p.positions[my_row];
-    float2 cs[kRows];
+    float w[4];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i)
-      cs[i] = p.rope[static_cast<size_t>(__shfl(positions, i)) * 64 + lane];
+    for (int c = 0; c < 4; ++c)
+      w[c] = weight[32 * c + j];
+    // Issue every position and rotary load before the arithmetic.
+    int position[8];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      const int r = wave + 8 * i;
-      const int m = m0 + r;
-      if (m >= p.m)
-        break;
-      const float v0 = tile[r * kPitch + lane];
-      const float v1 = tile[r * kPitch + lane + 64];
-      const float squares = WaveSumFast(v0 * v0 + v1 * v1);
+    for (int e = 0; e < 8; ++e)
+      position[e] = p.positions[min(row0 + RowOf(e, lane), p.m - 1)];
+    float2 cs[8][2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        cs[e][c] = p.rope[static_cast<size_t>(position[e]) * 64 + 32 * c + j];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int m = row0 + RowOf(e, lane);
+      float squares = o.v[0][e] * o.v[0][e];
+#pragma unroll
+      for (int c = 1; c < 4; ++c)
+        squares += o.v[c][e] * o.v[c][e];
+      squares = HalfWaveSum(squares);
       const float scale = rsqrtf(squares * (1.0F / 128.0F) + p.eps);
-      const float a = w0 * (v0 * scale);
-      const float b = w1 * (v1 * scale);
+      if (m >= p.m)
+        continue;
       half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
-      out[lane] = static_cast<half_t>(a * cs[i].x - b * cs[i].y);
-      out[lane + 64] = static_cast<half_t>(b * cs[i].x + a * cs[i].y);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float a = w[c] * (o.v[c][e] * scale);
+        const float b = w[c + 2] * (o.v[c + 2][e] * scale);
+        out[32 * c + j] = static_cast<half_t>(a * cs[e][c].x - b * cs[e][c].y);
+        out[32 * c + j + 64] =
+            static_cast<half_t>(b * cs[e][c].x + a * cs[e][c].y);
+      }
     }
     return;
   }
-  // Value heads: V^T[g][d][row], four consecutive rows per 8-byte store.
+  // Value heads: V^T[g][d][row]; e = 4 h .. 4 h + 3 are consecutive rows.
   const int g = slot - p.heads - p.kv_heads;
-  const int d = threadIdx.x & 127;
-  half_t* out = p.vt + static_cast<size_t>(g * 128 + d) * p.ldvt;
-  for (int q = threadIdx.x >> 7; q < kBM / 4; q += kThreads / 128) {
-    const int m = m0 + 4 * q;
-    if (m >= p.m)
-      break;
-    const half4 v = {static_cast<half_t>(tile[(4 * q) * kPitch + d]),
-                     static_cast<half_t>(tile[(4 * q + 1) * kPitch + d]),
-                     static_cast<half_t>(tile[(4 * q + 2) * kPitch + d]),
-                     static_cast<half_t>(tile[(4 * q + 3) * kPitch + d])};
-    if (m + 3 < p.m) {
-      *reinterpret_cast<half4*>(out + m) = v;
-    } else {
-      for (int e = 0; e < 4 && m + e < p.m; ++e)
-        out[m + e] = v[e];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    half_t* out = p.vt + static_cast<size_t>(g * 128 + 32 * c + j) * p.ldvt;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = row0 + RowOf(4 * h, lane);
+      const half4 v = {static_cast<half_t>(o.v[c][4 * h]),
+                       static_cast<half_t>(o.v[c][4 * h + 1]),
+                       static_cast<half_t>(o.v[c][4 * h + 2]),
+                       static_cast<half_t>(o.v[c][4 * h + 3])};
+      if (m + 3 < p.m) {
+        *reinterpret_cast<half4*>(out + m) = v;
+      } else {
+        for (int e = 0; e < 4 && m + e < p.m; ++e)
+          out[m + e] = v[e];
+      }
     }
   }
 }
 
-__device__ __forceinline__ void SwiGluRows(const GemmParams& p,
-                                           const float* tile, int m0,
-                                           int tile_n) {
+__device__ __forceinline__ void SwiGluOwned(const GemmParams& p,
+                                            const Owned& o, int row0,
+                                            int tile_n) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int r = wave; r < kBM; r += kThreads / 64) {
-    const int m = m0 + r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int m = row0 + RowOf(e, lane);
     if (m >= p.m)
-      break;
-    const float g = tile[r * kPitch + lane];
-    const float u = tile[r * kPitch + lane + 64];
-    p.act[static_cast<size_t>(m) * p.ldh + tile_n * 64 + lane] =
-        static_cast<half_t>(g / (1.0F + __expf(-g)) * u);
+      continue;
+    half_t* out = p.act + static_cast<size_t>(m) * p.ldh + tile_n * 64 + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float g = o.v[c][e];
+      const float u = o.v[c + 2][e];
+      out[32 * c] = static_cast<half_t>(g / (1.0F + __expf(-g)) * u);
+    }
   }
 }
 
 template <Epilogue EPI>
-__device__ __forceinline__ void TileEpilogue(const GemmParams& p,
-                                             const float* tile, int tile_m,
-                                             int tile_n) {
-  const int m0 = tile_m * kBM;
-  if constexpr (EPI == Epilogue::kStore || EPI == Epilogue::kPartial)
-    StoreRows(p, tile, m0, tile_n * kBN, false);
+__device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
+                                              const Owned& o, int row0,
+                                              int tile_n) {
+  if constexpr (EPI == Epilogue::kStore)
+    StoreOwned(p, o, p.y, row0, tile_n * kBN, false);
   else if constexpr (EPI == Epilogue::kAccumulate)
-    StoreRows(p, tile, m0, tile_n * kBN, true);
+    StoreOwned(p, o, p.y, row0, tile_n * kBN, true);
   else if constexpr (EPI == Epilogue::kQkvRope)
-    QkvRows(p, tile, m0, tile_n);
-  else
-    SwiGluRows(p, tile, m0, tile_n);
+    QkvOwned(p, o, row0, tile_n);
+  else if constexpr (EPI == Epilogue::kSwiGlu)
+    SwiGluOwned(p, o, row0, tile_n);
 }
 
 // ------------------------------------------------------------- main kernel
@@ -253,55 +281,108 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int group = wave >> 2;         // K substeps 2 group, 2 group + 1
-  const int wave_m = (wave >> 1) & 1;  // 64-row half of the tile
-  const int wave_n = wave & 1;         // 64-column half
+  // Wave-uniform, so that everything derived from it stays scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = wave >> 2;  // K substeps 2 group, 2 group + 1
+  const int wave_m = wave & 3;  // rows 32 wave_m .. 32 wave_m + 31
 
   // DMA sources: wave w fills 1 KB blocks w * kAInstr + i of A (8 rows each)
   // and of B; lane l brings row 8 b + l / 8 at LDS position l % 8, i.e.
   // chunk Swizzle(row, l % 8). Rows past M or N read the last valid row
   // (their results are never stored).
-  const half_t* a_src[kAInstr];
-  const half_t* b_src[kBInstr];
+  uint32_t a_src[kAInstr], b_src[kBInstr];  // byte offsets from the bases
 #pragma unroll
   for (int i = 0; i < kAInstr; ++i) {
     const int row = (wave * kAInstr + i) * 8 + (lane >> 3);
-    a_src[i] = p.x + static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda +
-               k_begin + Swizzle(row, lane & 7) * 8;
+    a_src[i] = static_cast<uint32_t>(min(m0 + row, p.m - 1)) * p.lda * 2 +
+               Swizzle(row, lane & 7) * 16;
   }
 #pragma unroll
   for (int i = 0; i < kBInstr; ++i) {
     const int row = (wave * kBInstr + i) * 8 + (lane >> 3);
-    b_src[i] = p.w + static_cast<size_t>(min(n0 + row, p.n - 1)) * p.ldb +
-               k_begin + Swizzle(row, lane & 7) * 8;
+    b_src[i] = static_cast<uint32_t>(min(n0 + row, p.n - 1)) * p.ldb * 2 +
+               Swizzle(row, lane & 7) * 16;
   }
+  const unsigned char* a_base =
+      reinterpret_cast<const unsigned char*>(p.x) + k_begin * 2;
+  const unsigned char* b_base =
+      reinterpret_cast<const unsigned char*>(p.w) + k_begin * 2;
   const uint32_t lds_base = LdsAddress(lds);
   auto issue = [&](int stage, int kt) {
     const uint32_t base = lds_base + stage * kStageBytes;
-    const int kk = kt * kBK;
+    const int kk = kt * kBK * 2;
 #pragma unroll
     for (int i = 0; i < kAInstr; ++i)
-      DmaToLds(a_src[i] + kk, base + (wave * kAInstr + i) * 1024);
+      DmaToLds(a_base + kk, a_src[i], base + (wave * kAInstr + i) * 1024);
 #pragma unroll
     for (int i = 0; i < kBInstr; ++i)
-      DmaToLds(b_src[i] + kk, base + kABytes + (wave * kBInstr + i) * 1024);
+      DmaToLds(b_base + kk, b_src[i],
+               base + kABytes + (wave * kBInstr + i) * 1024);
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[4];
 #pragma unroll
-  for (int fm = 0; fm < 2; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < 2; ++fn)
-      acc[fm][fn] = floatx16{};
+  for (int c = 0; c < 4; ++c)
+    acc[c] = floatx16{};
 
+  // Byte offsets of this lane's fragments inside a stage (stage-invariant):
+  // A rows of the wave's strip, B rows 32 c + (lane & 31) for column block c.
+  int a_off[2], b_off[2][4];
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int j = 0; j < 2; ++j) {
+    const int chunk = 2 * (2 * group + j) + (lane >> 5);
+    const int ra = wave_m * 32 + (lane & 31);
+    a_off[j] = ra * 128 + Swizzle(ra, chunk) * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int rb = c * 32 + (lane & 31);
+      b_off[j][c] = kABytes + rb * 128 + Swizzle(rb, chunk) * 16;
+    }
+  }
+  struct Fragments {
+    half8 a[2], b[2][4];
+  };
+  auto read = [&](int kt) {
+    const unsigned char* s = lds + (kt % STAGES) * kStageBytes;
+    Fragments fr;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      fr.a[j] = *reinterpret_cast<const half8*>(s + a_off[j]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        fr.b[j][c] = *reinterpret_cast<const half8*>(s + b_off[j][c]);
+    }
+    return fr;
+  };
+
+  // The ring: stage kt lives in buffer kt % STAGES. All buffers are filled
+  // up front; in step kt, once stage kt + 1 has landed and every wave has
+  // finished reading stage kt (its fragments are in registers), stage
+  // kt + STAGES is loaded into kt's buffer, and stage kt + 1's fragments are
+  // read while stage kt's MFMAs run.
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
     if (s < steps)
       issue(s, s);
-  for (int kt = 0; kt < steps; ++kt) {
-    // Stage kt has landed once at most `ahead` later stages are in flight.
-    const int ahead = min(STAGES - 2, steps - 1 - kt);
+  {
+    const int ahead = min(STAGES, steps) - 1;  // stages after 0 in flight
+    if (ahead >= 3)
+      WaitLoads<3 * kLoads>();
+    else if (ahead == 2)
+      WaitLoads<2 * kLoads>();
+    else if (ahead == 1)
+      WaitLoads<kLoads>();
+    else
+      WaitLoads<0>();
+  }
+  StageBarrier();
+  // Makes stage kt + 1 readable and refills kt's buffer: stages up to
+  // min(kt + STAGES - 1, steps - 1) are issued, so stage kt + 1 has landed
+  // once at most `ahead` later ones are in flight; the barrier also tells
+  // that every wave's fragment reads of stage kt have completed.
+  auto advance = [&](int kt) {
+    const int ahead = min(STAGES - 2, steps - 2 - kt);
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     if (ahead >= 2)
       WaitLoads<2 * kLoads>();
     else if (ahead == 1)
@@ -309,98 +390,125 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     else
       WaitLoads<0>();
     StageBarrier();
-    // Every wave is past its reads of stage kt - 1: refill that buffer.
-    if (kt + STAGES - 1 < steps)
-      issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
-    const unsigned char* as = lds + (kt % STAGES) * kStageBytes;
-    const unsigned char* bs = as + kABytes;
-    half8 a[2][2], b[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int chunk = 2 * (2 * group + j) + (lane >> 5);
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const int ra = wave_m * 64 + f * 32 + (lane & 31);
-        a[j][f] = *reinterpret_cast<const half8*>(as + ra * 128 +
-                                                  Swizzle(ra, chunk) * 16);
-        const int rb = wave_n * 64 + f * 32 + (lane & 31);
-        b[j][f] = *reinterpret_cast<const half8*>(bs + rb * 128 +
-                                                  Swizzle(rb, chunk) * 16);
-      }
-    }
+    if (kt + STAGES < steps)
+      issue(kt % STAGES, kt + STAGES);
+  };
+  // The scheduling barrier keeps the compiler from hoisting the next
+  // advance's wait above these MFMAs, which would stall them behind the
+  // reads they are meant to overlap.
+  auto mma = [&](const Fragments& fr) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int fm = 0; fm < 2; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < 2; ++fn)
-          acc[fm][fn] = Mfma32(a[j][fm], b[j][fn], acc[fm][fn]);
+      for (int c = 0; c < 4; ++c)
+        acc[c] = Mfma32(fr.a[j], fr.b[j][c], acc[c]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Two fragment sets in ping-pong, so that a step's MFMAs never wait for
+  // the next step's LDS reads, which are issued just before them.
+  // The loop body has no branch around reads: a read on only one path makes
+  // the compiler wait for it on both.
+  Fragments even = read(0), odd;
+  int kt = 0;
+  for (; kt + 2 < steps; kt += 2) {
+    advance(kt);
+    odd = read(kt + 1);
+    mma(even);
+    advance(kt + 1);
+    even = read(kt + 2);
+    mma(odd);
+  }
+  if (kt + 1 < steps) {
+    advance(kt);
+    odd = read(kt + 1);
+    mma(even);
+    mma(odd);
+  } else {
+    mma(even);
   }
 
-  // Sum the groups into the fp32 tile: group 1 stores, group 0 adds its own
-  // accumulators to what group 1 left (group 0 + group 1).
-  __syncthreads();
-  float* tile_lds = reinterpret_cast<float*>(lds);
+  // Swap accumulator halves: group g keeps elements 8 g .. 8 g + 7 (rows
+  // 16 g .. 16 g + 15 of the strip) and hands the other eight to its partner
+  // wave ^ 4, as float4 q = 2 c + h at ((wave * 8 + q) * 64 + lane) * 16.
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  StageBarrier();
+  {
+    floatx4* mine = reinterpret_cast<floatx4*>(lds) + wave * 8 * 64 + lane;
+    const int give = 8 * (1 - group);
 #pragma unroll
-  for (int phase = 1; phase >= 0; --phase) {
-    if (group == phase) {
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int fm = 0; fm < 2; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < 2; ++fn)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = wave_m * 64 + fm * 32 + 8 * (r / 4) +
-                            4 * (lane >> 5) + (r & 3);
-            const int col = wave_n * 64 + fn * 32 + (lane & 31);
-            float* cell = tile_lds + row * kPitch + col;
-            *cell = phase == 1 ? acc[fm][fn][r] : acc[fm][fn][r] + *cell;
-          }
-    }
-    __syncthreads();
+      for (int h = 0; h < 2; ++h)
+        mine[(2 * c + h) * 64] = floatx4{acc[c][give + 4 * h],
+                                         acc[c][give + 4 * h + 1],
+                                         acc[c][give + 4 * h + 2],
+                                         acc[c][give + 4 * h + 3]};
   }
+  __syncthreads();
+  Owned own;
+  {
+    const floatx4* theirs =
+        reinterpret_cast<const floatx4*>(lds) + (wave ^ 4) * 8 * 64 + lane;
+    const int keep = 8 * group;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const floatx4 t = theirs[(2 * c + h) * 64];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          own.v[c][4 * h + i] = acc[c][keep + 4 * h + i] + t[i];
+      }
+  }
+  const int row0 = m0 + 32 * wave_m + 16 * group;
 
   if constexpr (EPI == Epilogue::kPartial) {
     // Each split owns a full [M][ldc] slice; the row kernel that consumes
     // the GEMM adds the slices.
-    GemmParams q = p;
-    q.y = p.y + static_cast<size_t>(split) * p.split_stride;
-    TileEpilogue<EPI>(q, tile_lds, tile_m, tile_n);
+    StoreOwned(p, own, p.y + static_cast<size_t>(split) * p.split_stride,
+               row0, n0, false);
     return;
   }
   if (p.splits > 1) {
-    float* mine = p.partials +
-                  (static_cast<size_t>(tile) * p.splits + split) * kTileFloats;
-    for (int f = tid; f < kTileFloats / 4; f += kThreads) {
-      const int row = f >> 5, c4 = (f & 31) * 4;
-      *reinterpret_cast<floatx4*>(mine + row * kBN + c4) =
-          *reinterpret_cast<const floatx4*>(tile_lds + row * kPitch + c4);
-    }
+    floatx4* mine = reinterpret_cast<floatx4*>(p.partials) +
+                    ((static_cast<size_t>(tile) * p.splits + split) * 8 + wave) * 8 * 64 +
+                    lane;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        mine[(2 * c + h) * 64] = floatx4{own.v[c][4 * h], own.v[c][4 * h + 1],
+                                         own.v[c][4 * h + 2], own.v[c][4 * h + 3]};
     return;
   }
-  TileEpilogue<EPI>(p, tile_lds, tile_m, tile_n);
+  OwnedEpilogue<EPI>(p, own, row0, tile_n);
 }
 
 // Sums a tile's split-K partials in split order 0, 1, ... (a fixed order,
-// reproducible bit for bit) into the LDS tile and applies the epilogue.
+// reproducible bit for bit) in the same per-wave layout the GEMM kernel
+// stored them in, and applies the epilogue.
 template <Epilogue EPI>
 __global__ __launch_bounds__(kThreads) void SplitReduceKernel(GemmParams p,
                                                               int tiles_m) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  float* tile_lds = reinterpret_cast<float*>(lds);
   const int tile = blockIdx.x;
-  const float* base =
-      p.partials + static_cast<size_t>(tile) * p.splits * kTileFloats;
-  for (int f = threadIdx.x; f < kTileFloats / 4; f += kThreads) {
-    const int row = f >> 5, c4 = (f & 31) * 4;
-    floatx4 sum = *reinterpret_cast<const floatx4*>(base + row * kBN + c4);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const floatx4* base = reinterpret_cast<const floatx4*>(p.partials) +
+                        (static_cast<size_t>(tile) * p.splits * 8 + wave) * 8 * 64 +
+                        lane;
+  Owned own;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    floatx4 sum = base[q * 64];
     for (int s = 1; s < p.splits; ++s)
-      sum += *reinterpret_cast<const floatx4*>(
-          base + static_cast<size_t>(s) * kTileFloats + row * kBN + c4);
-    *reinterpret_cast<floatx4*>(tile_lds + row * kPitch + c4) = sum;
+      sum += base[static_cast<size_t>(s) * 8 * 8 * 64 + q * 64];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      own.v[q >> 1][4 * (q & 1) + i] = sum[i];
   }
-  __syncthreads();
-  TileEpilogue<EPI>(p, tile_lds, tile % tiles_m, tile / tiles_m);
+  const int tile_m = tile % tiles_m;
+  const int row0 = tile_m * kBM + 32 * (wave & 3) + 16 * (wave >> 2);
+  OwnedEpilogue<EPI>(p, own, row0, tile / tiles_m);
 }
 
 template <int STAGES, Epilogue EPI>
@@ -408,8 +516,8 @@ void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
   GemmKernel<STAGES, EPI>
       <<<dim3(groups), dim3(kThreads), LdsBytes<STAGES>(), stream>>>(p, tiles_m);
   if (p.splits > 1 && EPI != Epilogue::kPartial)
-    SplitReduceKernel<EPI><<<dim3(groups / p.splits), dim3(kThreads),
-                             kEpilogueBytes, stream>>>(p, tiles_m);
+    SplitReduceKernel<EPI><<<dim3(groups / p.splits), dim3(kThreads), 0,
+                             stream>>>(p, tiles_m);
 }
 
 template <Epilogue EPI>
@@ -476,6 +584,10 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
           "gemm: plan does not match the shape");
   Require(p.lda % 8 == 0 && p.ldb % 8 == 0,
           "gemm: leading dimensions must be multiples of 8");
+  // DMA sources are 32-bit byte offsets from the operand bases.
+  Require(static_cast<uint64_t>(p.m) * p.lda * 2 < (uint64_t{1} << 32) &&
+              static_cast<uint64_t>(p.n) * p.ldb * 2 < (uint64_t{1} << 32),
+          "gemm: operands must be under 4 GiB");
   Require(plan.splits == 1 || epilogue == Epilogue::kPartial ||
               p.partials != nullptr,
           "gemm: split-K needs a partials buffer");

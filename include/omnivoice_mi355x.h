@@ -251,7 +251,7 @@ int ovg_op_rmsnorm(const float* input, const float* weight, void* output,
  * State::Attention calls plus MergeHeads (reference: generator.cpp:122-172,
  * generator_kernels.hpp:44-47). qkv is fp16 [rows][(heads + 2*kv_heads) *
  * 128] after q/k norm and rotary; `sequences` holds `count` (first_row,
- * length) pairs (first_row a multiple of 8); output fp16 [rows][heads*128]. */
+ * length) pairs (first_row a multiple of 16); output fp16 [rows][heads*128]. */
 int ovg_op_attention(const void* qkv, void* output, int64_t rows,
                      int64_t heads, int64_t kv_heads,
                      const int64_t* sequences, int64_t count, void* stream,

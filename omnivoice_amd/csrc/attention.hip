@@ -5,22 +5,29 @@
 // 161-189). Scores never leave registers.
 //
 // A work-group takes one tile of 32 queries of one sequence and one key/value
-// head g. Its 2 x GROUP waves are the GROUP query heads of g times two key
-// halves: keys are staged in LDS as pairs of 32-key tiles (K [32][128] and
-// V^T [128][32] each), the first tile of a pair for key-half 0, the second
-// for key-half 1, so each K/V tile is read from memory once for the whole
-// head group (no GQA repeat). The next pair is prefetched into registers
-// while the current one is used (double-buffered LDS, one barrier per pair).
-// At the end the two key halves' online-softmax states merge through LDS.
+// head g, with 4 x GROUP compute waves (the GROUP query heads of g times four
+// key quarters) and one producer wave. Keys come in 32-key tiles (K [32][128]
+// and V^T [128][32], 16 KB), fetched global -> LDS by DMA into an 8-slot
+// ring, four tiles (a round) at a time; the producer fetches round r + 1
+// while the compute waves work on round r, quarter q taking tile 4 r + q.
+// Each tile is read from memory once for the whole head group (no GQA
+// repeat), and the group's query tiles come into LDS the same way, once. At
+// the end every wave leaves its online-softmax state in LDS and wave
+// (head, quarter q) merges the four quarters' states for dims 32 q .. 32 q +
+// 31 of its head in a fixed order, ((0 + 1) + (2 + 3)), and stores them.
 //
 // Scores are formed transposed, S^T = K Q^T (keys as MFMA rows, queries as
 // columns), so that every lane owns one query column: the running max and
 // sum are per-lane values combined with the partner lane l ^ 32 only. The
 // value product is likewise transposed, O^T = V^T P^T: P^T is the score
-// accumulator itself converted to fp16 (the MFMA's k order is permuted to
-// the accumulator's row order, and V^T is read from LDS in the same order),
-// so probabilities never move between lanes. V^T comes pre-transposed from
-// the q/k/v GEMM's epilogue ([kv head][dim][row]).
+// accumulator itself converted to fp16, so probabilities never move between
+// lanes. Lane half h holds keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key
+// block; V^T arrives from the q/k/v epilogue with the keys of every 16-row
+// block stored in the order 0-3, 8-11, 4-7, 12-15 (VtColumn), which makes
+// those eight keys one 16-byte run.
+//
+// LDS rows are XOR-swizzled in 16-byte chunks (K: chunk ^ (key & 15); V^T:
+// chunk ^ ((dim >> 2) & 3)) so that both operand reads are conflict-free.
 #include "kernels.hpp"
 
 namespace ovg {
@@ -28,138 +35,244 @@ namespace {
 
 constexpr int kKTile = 32;
 constexpr int kHeadDim = 128;
-constexpr int kKPitch = kHeadDim + 8;  // halves per key row in LDS
-constexpr int kVPitch = kKTile + 8;    // halves per dim row of V^T in LDS
-constexpr int kKHalves = kKTile * kKPitch;
-constexpr int kVHalves = kHeadDim * kVPitch;
-constexpr int kTileHalves = kKHalves + kVHalves;  // one staged key tile
-constexpr int kChunksPerTile = 2 * kKTile * kHeadDim / 8;  // K + V^T, 16 B
+constexpr int kTileBytes = 16384;  // K (8 KB) then V^T (8 KB)
+constexpr int kSlots = 8;          // ring of 32-key tiles
+constexpr int kRound = 4;          // tiles per round = key quarters
+constexpr int kRingBytes = kSlots * kTileBytes;
+constexpr int kQBytes = 8192;      // one head's 32 x 128 query tile
+
+// Ring, then the group's query tiles; the merge reuses the space for every
+// wave's (max, sum) pairs and O^T accumulators (16 float4 per lane).
+template <int GROUP>
+constexpr int AttentionLds() {
+  const int ring = kRingBytes + GROUP * kQBytes;
+  const int merge = 4 * GROUP * 64 * (8 + 16 * 16);
+  return ring > merge ? ring : merge;
+}
+
+__device__ __forceinline__ uint32_t LdsAddress(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) unsigned char*)(p)));
+}
+
+// Wave-wide DMA of 64 x 16 bytes into LDS (lane l's bytes land at
+// lds_addr + 16 l) from a wave-uniform base plus a per-lane byte offset.
+__device__ __forceinline__ void DmaToLds(const unsigned char* base,
+                                         uint32_t offset, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(lds_addr), "v"(offset), "s"(base)
+      : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void WaitLoads() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Barrier without the fence of __syncthreads(), which would wait for every
+// DMA in flight.
+__device__ __forceinline__ void RingBarrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" : : : "memory");
+}
+
+struct State {
+  float max, sum;
+  floatx16 o[4];  // O^T: lane holds dims 32 dt + 8 (r / 4) + 4 h + r % 4
+};
+
+// One quarter's state restricted to a 32-dim slice.
+struct Slice {
+  float max, sum;
+  floatx16 o;
+};
+
+// a then b: a state with max -inf is empty and weighs zero.
+__device__ __forceinline__ Slice Merge(const Slice& a, const Slice& b) {
+  const float m = fmaxf(a.max, b.max);
+  const float wa = a.max == -__builtin_inff() ? 0.0F : __builtin_amdgcn_exp2f(a.max - m);
+  const float wb = b.max == -__builtin_inff() ? 0.0F : __builtin_amdgcn_exp2f(b.max - m);
+  Slice c;
+  c.max = m;
+  c.sum = a.sum * wa + b.sum * wb;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    c.o[r] = a.o[r] * wa + b.o[r] * wb;
+  return c;
+}
 
 template <int GROUP>
-__global__ __launch_bounds__(GROUP * 128) void AttentionKernel(
+__global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     AttentionParams p) {
-  constexpr int kThreads = GROUP * 128;
-  constexpr int kChunks = 2 * kChunksPerTile / kThreads;  // per thread per pair
-  // Two buffers of a tile pair; the merge area reuses them.
-  __shared__ __align__(16) half_t lds[2 * 2 * kTileHalves];
-  const AttentionWork work = p.work[blockIdx.x];
-  const int g = blockIdx.y;
+  constexpr int kWaves = 4 * GROUP;  // compute waves; wave kWaves feeds them
+  extern __shared__ __align__(16) unsigned char lds[];
+  // Work-groups go round-robin over the 8 XCDs: block b takes kv head
+  // b % kv_heads, so with 8 kv heads each XCD's L2 holds one head's keys,
+  // values and queries only.
+  const int g = blockIdx.x % p.kv_heads;
+  const AttentionWork work = p.work[blockIdx.x / p.kv_heads];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int head_local = wave % GROUP;
-  const int key_half = wave / GROUP;
+  const int quarter = wave / GROUP;
   const int head = g * GROUP + head_local;
   const int half_id = lane >> 5;
   const int col = lane & 31;
+  const int tiles = (work.seq_length + kKTile - 1) / kKTile;
+  const int rounds = (tiles + kRound - 1) / kRound;
 
+  // DMA plan: instruction i of a round (64 of them) loads 1 KB of tile
+  // 4 r + i / 16; part (i / 8) % 2 is K or V^T, sub = i % 8 its 1 KB block.
+  // One producer wave issues them all, so that no compute wave ever stalls
+  // on a full memory queue; tiles past the sequence reload its last tile.
+  const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
+      p.qk + (p.heads + g) * kHeadDim);
+  const unsigned char* v_base = reinterpret_cast<const unsigned char*>(
+      p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt);
+  // Lane offsets: K row 4 sub + lane / 16 at swizzled chunk; V^T dim
+  // 16 sub + lane / 4 at chunk (lane & 3) ^ ((lane >> 4) & 3).
+  uint32_t k_lane[8];
+#pragma unroll
+  for (int sub = 0; sub < 8; ++sub) {
+    const int key = 4 * sub + (lane >> 4);
+    const int chunk = (lane & 15) ^ (key & 15);
+    k_lane[sub] = static_cast<uint32_t>((lane >> 4) * p.ld_qk + 8 * chunk) * 2;
+  }
+  const uint32_t v_lane = static_cast<uint32_t>(
+      (lane >> 2) * p.ldvt + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
+  const uint32_t lds_base = LdsAddress(lds);
+  // The r-th round processed is key round (r + shift) % rounds: work-groups
+  // of the same head start on different rounds, so they do not all pull the
+  // same L2 lines at once. Its tiles go to ring half r % 2.
+  const int shift = (blockIdx.x / p.kv_heads) % rounds;
+  auto round_of = [&](int r) {
+    const int k = r + shift;
+    return k >= rounds ? k - rounds : k;
+  };
+  auto issue = [&](int r) {
+    const int round = round_of(r);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int slot_in_round = i / 16;
+      const int part = (i / 8) & 1;
+      const int sub = i & 7;
+      const int t = min(round * kRound + slot_in_round, tiles - 1);
+      const int key0 = work.seq_begin + t * kKTile;
+      const uint32_t dst = lds_base + ((r & 1) * kRound + slot_in_round) * kTileBytes +
+                           part * 8192 + sub * 1024;
+      if (part == 0) {
+        DmaToLds(k_base + static_cast<size_t>(key0 + 4 * sub) * p.ld_qk * 2,
+                 k_lane[sub], dst);
+      } else {
+        DmaToLds(v_base + (static_cast<size_t>(16 * sub) * p.ldvt + key0) * 2,
+                 v_lane, dst);
+      }
+    }
+  };
+
+  if (wave == kWaves) {
+    // The producer: the group's query tiles (laid out like a K tile; query
+    // rows past the tile's count repeat its last row, whose results are
+    // never stored) and round 0, then round r + 1 while round r is computed.
+    // Its barriers pair one to one with the compute waves'.
+#pragma unroll
+    for (int i = 0; i < 8 * GROUP; ++i) {
+      const int h = i >> 3, sub = i & 7;
+      const int row = min(4 * sub + (lane >> 4), work.q_count - 1);
+      const int chunk = (lane & 15) ^ ((4 * sub + (lane >> 4)) & 15);
+      DmaToLds(reinterpret_cast<const unsigned char*>(
+                   p.qk + static_cast<size_t>(work.q_begin) * p.ld_qk +
+                   (g * GROUP + h) * kHeadDim),
+               static_cast<uint32_t>(row * p.ld_qk + 8 * chunk) * 2,
+               lds_base + kRingBytes + h * kQBytes + sub * 1024);
+    }
+    issue(0);
+    WaitLoads<0>();
+    RingBarrier();
+    for (int r = 0; r < rounds; ++r) {
+      if (r + 1 < rounds) {
+        issue(r + 1);
+        WaitLoads<0>();
+      }
+      RingBarrier();
+    }
+    __syncthreads();
+    __syncthreads();
+    return;
+  }
+  State st;
+  st.max = -__builtin_inff();
+  st.sum = 0.0F;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    st.o[dt] = floatx16{};
+
+  // Stage-invariant LDS read offsets.
+  int k_read[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    k_read[kk] = col * 256 + (((2 * kk + half_id) ^ (col & 15)) * 16);
+  int v_read[4][2];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const int d = 32 * dt + col;
+#pragma unroll
+    for (int j2 = 0; j2 < 2; ++j2)
+      v_read[dt][j2] = 8192 + d * 64 + (((2 * j2 + half_id) ^ ((d >> 2) & 3)) * 16);
+  }
+
+  // Barrier r: round r has landed (the producer waited for it) and every
+  // compute wave is done with round r - 1, whose ring half the producer
+  // refills with round r + 1 meanwhile.
+  RingBarrier();
   // Q^T operand: lane supplies dims 16 kk + 8 half_id .. +7 of query col.
   half8 qf[8];
   {
-    const bool valid = col < work.q_count;
-    const half_t* q = p.qk + static_cast<size_t>(work.q_begin + col) * p.ld_qk +
-                      head * kHeadDim + half_id * 8;
+    const unsigned char* qs = lds + kRingBytes + head_local * kQBytes;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
-      qf[kk] = valid ? *reinterpret_cast<const half8*>(q + kk * 16)
-                     : half8{0, 0, 0, 0, 0, 0, 0, 0};
+      qf[kk] = *reinterpret_cast<const half8*>(qs + k_read[kk]);
   }
-  floatx16 ot[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-    ot[dt] = floatx16{};
-  float run_max = -__builtin_inff();
-  float run_sum = 0.0F;
-
-  const half_t* kbase = p.qk + (p.heads + g) * kHeadDim;
-  const half_t* vbase = p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt;
-  const int tiles = (work.seq_length + kKTile - 1) / kKTile;
-  const int pairs = (tiles + 1) / 2;
-
-  // Chunk c of a pair: tile c / kChunksPerTile; within a tile the first 512
-  // chunks are K rows (16 per key), the rest V^T rows (4 per dim).
-  half8 staged[kChunks];
-  auto load = [&](int pair) {
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-      const int c = tid + j * kThreads;
-      const int t = 2 * pair + c / kChunksPerTile;
-      const int ci = c % kChunksPerTile;
-      const int key0 = work.seq_begin + t * kKTile;
-      if (t >= tiles)
-        continue;
-      if (ci < kChunksPerTile / 2) {
-        staged[j] = *reinterpret_cast<const half8*>(
-            kbase + static_cast<size_t>(key0 + (ci >> 4)) * p.ld_qk + (ci & 15) * 8);
-      } else {
-        const int cv = ci - kChunksPerTile / 2;
-        staged[j] = *reinterpret_cast<const half8*>(
-            vbase + static_cast<size_t>(cv >> 2) * p.ldvt + key0 + (cv & 3) * 8);
-      }
-    }
-  };
-  auto store = [&](int pair, int buffer) {
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-      const int c = tid + j * kThreads;
-      const int slot = c / kChunksPerTile;
-      const int ci = c % kChunksPerTile;
-      if (2 * pair + slot >= tiles)
-        continue;
-      half_t* tile_lds = lds + (buffer * 2 + slot) * kTileHalves;
-      if (ci < kChunksPerTile / 2) {
-        *reinterpret_cast<half8*>(tile_lds + (ci >> 4) * kKPitch + (ci & 15) * 8) =
-            staged[j];
-      } else {
-        const int cv = ci - kChunksPerTile / 2;
-        *reinterpret_cast<half8*>(tile_lds + kKHalves + (cv >> 2) * kVPitch +
-                                  (cv & 3) * 8) = staged[j];
-      }
-    }
-  };
-
-  load(0);
-  store(0, 0);
-  __syncthreads();
-  for (int pair = 0; pair < pairs; ++pair) {
-    if (pair + 1 < pairs)
-      load(pair + 1);
-    const int t = 2 * pair + key_half;
+  for (int r = 0; r < rounds; ++r) {
+    const int t = round_of(r) * kRound + quarter;
     if (t < tiles) {
-      const half_t* ks = lds + ((pair & 1) * 2 + key_half) * kTileHalves;
-      const half_t* vs = ks + kKHalves;
+      const unsigned char* tile = lds + ((r & 1) * kRound + quarter) * kTileBytes;
       floatx16 s = floatx16{};
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const half8 kf = *reinterpret_cast<const half8*>(
-            ks + col * kKPitch + kk * 16 + half_id * 8);
-        s = Mfma32(kf, qf[kk], s);
-      }
+      for (int kk = 0; kk < 8; ++kk)
+        s = Mfma32(*reinterpret_cast<const half8*>(tile + k_read[kk]), qf[kk], s);
       // Lane holds keys 8 (r / 4) + 4 half_id + r % 4 of its query column.
       const int valid_keys = work.seq_length - t * kKTile;
       float tile_max = -__builtin_inff();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r / 4) + 4 * half_id + (r & 3);
-        s[r] = key < valid_keys ? s[r] * p.scale_log2 : -__builtin_inff();
-        tile_max = fmaxf(tile_max, s[r]);
+      for (int e = 0; e < 16; ++e) {
+        const int key = 8 * (e / 4) + 4 * half_id + (e & 3);
+        s[e] = key < valid_keys ? s[e] * p.scale_log2 : -__builtin_inff();
+        tile_max = fmaxf(tile_max, s[e]);
       }
       tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-      const float new_max = fmaxf(run_max, tile_max);
-      const float alpha = __builtin_amdgcn_exp2f(run_max - new_max);
-      run_max = new_max;
+      const float new_max = fmaxf(st.max, tile_max);
+      const float alpha = __builtin_amdgcn_exp2f(st.max - new_max);
+      st.max = new_max;
       float psum = 0.0F;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = __builtin_amdgcn_exp2f(s[r] - new_max);
-        psum += s[r];
+      for (int e = 0; e < 16; ++e) {
+        s[e] = __builtin_amdgcn_exp2f(s[e] - new_max);
+        psum += s[e];
       }
-      run_sum = run_sum * alpha + psum;
+      st.sum = st.sum * alpha + psum;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
-        ot[dt] *= alpha;
-      // P^T operand for keys 16 j2 .. 16 j2 + 15: slot e <-> accumulator
-      // element 8 j2 + e, i.e. key 16 j2 + (e < 4 ? 4 h + e : 8 + 4 h + e - 4).
+        st.o[dt] *= alpha;
+      // P^T operand for keys 16 j2 .. 16 j2 + 15: slot e is accumulator
+      // element 8 j2 + e; V^T's permuted block order puts the same keys in
+      // the 16 bytes at position 8 half_id of the block.
 #pragma unroll
       for (int j2 = 0; j2 < 2; ++j2) {
         half8 pb;
@@ -167,60 +280,60 @@ __global__ __launch_bounds__(GROUP * 128) void AttentionKernel(
         for (int e = 0; e < 8; ++e)
           pb[e] = static_cast<half_t>(s[8 * j2 + e]);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const half_t* vrow = vs + (dt * 32 + col) * kVPitch + 16 * j2 + 4 * half_id;
-          const half4 lo = *reinterpret_cast<const half4*>(vrow);
-          const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
-          const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          ot[dt] = Mfma32(va, pb, ot[dt]);
-        }
+        for (int dt = 0; dt < 4; ++dt)
+          st.o[dt] = Mfma32(*reinterpret_cast<const half8*>(tile + v_read[dt][j2]),
+                            pb, st.o[dt]);
       }
     }
-    if (pair + 1 < pairs)
-      store(pair + 1, (pair + 1) & 1);
-    __syncthreads();
+    RingBarrier();  // barrier r + 1
   }
 
-  // Merge the key halves: half 1 leaves (max, sum, O) per lane in LDS.
-  float* merge = reinterpret_cast<float*>(lds);
-  float* mine = merge + (head_local * 64 + lane) * 66;
-  if (key_half == 1) {
-    mine[0] = run_max;
-    mine[1] = run_sum;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        mine[2 + dt * 16 + r] = ot[dt][r];
-  }
+  // Every wave leaves (max, sum) as a float2 and O^T as 16 float4 per lane;
+  // wave (head, quarter) then merges dims 32 quarter .. +31 of its head.
+  float2* pairs = reinterpret_cast<float2*>(lds);
+  floatx4* accs = reinterpret_cast<floatx4*>(lds + kWaves * 64 * 8);
   __syncthreads();
-  if (key_half == 1)
-    return;
-  const float other_max = mine[0];
-  const float new_max = fmaxf(run_max, other_max);
-  const float a0 = __builtin_amdgcn_exp2f(run_max - new_max);
-  const float a1 = __builtin_amdgcn_exp2f(other_max - new_max);
-  const float sum = run_sum * a0 + mine[1] * a1;
-  const float total = sum + __shfl_xor(sum, 32);
+  pairs[wave * 64 + lane] = float2{st.max, st.sum};
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      accs[(wave * 16 + dt * 4 + k) * 64 + lane] =
+          floatx4{st.o[dt][4 * k], st.o[dt][4 * k + 1], st.o[dt][4 * k + 2],
+                  st.o[dt][4 * k + 3]};
+  __syncthreads();
+  const int dt = quarter;
+  auto load = [&](int q) {
+    const int w = q * GROUP + head_local;
+    const float2 ms = pairs[w * 64 + lane];
+    Slice sl;
+    sl.max = ms.x;
+    sl.sum = ms.y;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const floatx4 v = accs[(w * 16 + dt * 4 + k) * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sl.o[4 * k + i] = v[i];
+    }
+    return sl;
+  };
+  const Slice final_state = Merge(Merge(load(0), load(1)), Merge(load(2), load(3)));
+  const float total = final_state.sum + __shfl_xor(final_state.sum, 32);
   const float inverse = 1.0F / total;
   if (col >= work.q_count)
     return;
   half_t* out = p.out + static_cast<size_t>(work.q_begin + col) * p.heads * kHeadDim +
-                head * kHeadDim;
-  // O^T accumulator dt: lane holds dims dt*32 + 8 (r / 4) + 4 half_id + r % 4.
+                head * kHeadDim + dt * 32;
+  // Lane holds dims 8 (r / 4) + 4 half_id + r % 4 of the slice.
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int q = 0; q < 4; ++q) {
+    half4 v;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      half4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * q + e;
-        v[e] = static_cast<half_t>(
-            (ot[dt][r] * a0 + mine[2 + dt * 16 + r] * a1) * inverse);
-      }
-      *reinterpret_cast<half4*>(out + dt * 32 + 8 * q + 4 * half_id) = v;
-    }
+    for (int e = 0; e < 4; ++e)
+      v[e] = static_cast<half_t>(final_state.o[4 * q + e] * inverse);
+    *reinterpret_cast<half4*>(out + 8 * q + 4 * half_id) = v;
+  }
 }
 
 }  // namespace
@@ -229,22 +342,22 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   Require(p.work_count > 0, "attention: no work");
   Require(p.kv_heads > 0 && p.heads % p.kv_heads == 0,
           "attention: heads must be a multiple of kv_heads");
-  Require(p.ld_qk % 8 == 0 && p.ldvt % 8 == 0,
-          "attention: leading dimensions must be multiples of 8");
+  Require(p.ld_qk % 8 == 0 && p.ldvt % 16 == 0,
+          "attention: ld_qk must be a multiple of 8 and ldvt of 16");
+  Require(static_cast<uint64_t>(p.ld_qk) * 2 * 64 < (uint64_t{1} << 31) &&
+              static_cast<uint64_t>(p.ldvt) * 2 * 64 < (uint64_t{1} << 31),
+          "attention: rows too wide");
   const int group = p.heads / p.kv_heads;
-  const dim3 grid(p.work_count, p.kv_heads);
+  const dim3 grid(p.work_count * p.kv_heads);
   switch (group) {
     case 1:
-      AttentionKernel<1><<<grid, dim3(128), 0, stream>>>(p);
+      AttentionKernel<1><<<grid, dim3(5 * 64), AttentionLds<1>(), stream>>>(p);
       break;
     case 2:
-      AttentionKernel<2><<<grid, dim3(256), 0, stream>>>(p);
-      break;
-    case 4:
-      AttentionKernel<4><<<grid, dim3(512), 0, stream>>>(p);
+      AttentionKernel<2><<<grid, dim3(9 * 64), AttentionLds<2>(), stream>>>(p);
       break;
     default:
-      throw Error("attention: query heads per kv head must be 1, 2 or 4");
+      throw Error("attention: query heads per kv head must be 1 or 2");
   }
   Check(hipGetLastError(), "attention launch");
 }

@@ -19,9 +19,17 @@ constexpr int kWave = 64;
 // Rows of every activation buffer are padded to this multiple (plus one
 // 32-row key tile of slack) so tile loads never leave the allocation.
 constexpr int kRowAlign = 256;
-// Each packed sequence starts at a multiple of this many rows, so that a
-// 32-key tile of V^T starts on a 16-byte boundary.
-constexpr int kSequenceAlign = 8;
+// Each packed sequence starts at a multiple of this many rows, so that its
+// 32-key tiles of V^T start on whole 16-row blocks (see VtColumn).
+constexpr int kSequenceAlign = 16;
+
+// Column of packed row `row` in V^T ([kv head][dim][column]): within every
+// 16-row block the rows are stored in the order 0-3, 8-11, 4-7, 12-15, the
+// key order of the attention kernel's probability operand.
+__host__ __device__ constexpr int VtColumn(int row) {
+  return (row & ~15) | (((row >> 2) & 1) << 3) | (((row >> 3) & 1) << 2) |
+         (row & 3);
+}
 
 __device__ __forceinline__ float WaveSum(float v) {
   for (int offset = kWave / 2; offset > 0; offset /= 2)

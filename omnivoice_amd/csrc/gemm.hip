@@ -198,7 +198,9 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
     }
     return;
   }
-  // Value heads: V^T[g][d][row]; e = 4 h .. 4 h + 3 are consecutive rows.
+  // Value heads: V^T[g][d][VtColumn(row)]; e = 4 h .. 4 h + 3 are four
+  // consecutive rows starting at a multiple of 4, which VtColumn keeps
+  // consecutive.
   const int g = slot - p.heads - p.kv_heads;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -211,10 +213,10 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
                        static_cast<half_t>(o.v[c][4 * h + 2]),
                        static_cast<half_t>(o.v[c][4 * h + 3])};
       if (m + 3 < p.m) {
-        *reinterpret_cast<half4*>(out + m) = v;
+        *reinterpret_cast<half4*>(out + VtColumn(m)) = v;
       } else {
         for (int e = 0; e < 4 && m + e < p.m; ++e)
-          out[m + e] = v[e];
+          out[VtColumn(m + e)] = v[e];
       }
     }
   }
@@ -602,7 +604,7 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
     case Epilogue::kQkvRope:
       Require(p.n == (p.heads + 2 * p.kv_heads) * 128,
               "gemm: q/k/v epilogue needs N = (heads + 2 kv_heads) * 128");
-      Require(p.ldvt % 4 == 0, "gemm: V^T rows must be 8-byte aligned");
+      Require(p.ldvt % 16 == 0, "gemm: V^T rows must hold whole 16-row blocks");
       LaunchEpi<Epilogue::kQkvRope>(p, plan, stream);
       break;
     case Epilogue::kSwiGlu:

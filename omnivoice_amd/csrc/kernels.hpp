@@ -36,7 +36,8 @@ enum class Epilogue : int {
   kStore = 0,       // y fp32 [M][ldc] = acc
   kAccumulate = 1,  // y fp32 [M][ldc] += acc (the residual stream)
   kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
-                    // qk [M][ldq]; v heads -> fp16 V^T vt[g][d][ldvt]
+                    // qk [M][ldq]; v heads -> fp16 V^T
+                    // vt[g][d][VtColumn(row)] (ldvt % 16 == 0)
   kSwiGlu = 3,      // W rows interleaved per 128-row tile as 64 gate rows
                     // then the matching 64 up rows; act fp16 [M][ldh] =
                     // silu(gate) * up
@@ -124,7 +125,7 @@ struct AddNormParams {
 };
 void LaunchAddNorm(const AddNormParams& p, hipStream_t stream);
 
-// vt[g][d][ldvt] = qkv[r][(heads + kv_heads + g) * 128 + d] for r < rows.
+// vt[g][d][VtColumn(r)] = qkv[r][(heads + kv_heads + g) * 128 + d], r < rows.
 void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
                       int rows, int heads, int kv_heads, hipStream_t stream);
 
@@ -136,7 +137,7 @@ struct AttentionWork {
 };
 struct AttentionParams {
   const half_t* qk;        // [rows][ld_qk]: q heads, then k heads
-  const half_t* vt;        // [kv_heads][128][ldvt]
+  const half_t* vt;        // [kv_heads][128][ldvt], columns by VtColumn
   half_t* out;             // [rows][heads * 128]
   const AttentionWork* work;
   int work_count;

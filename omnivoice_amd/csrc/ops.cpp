@@ -189,7 +189,7 @@ int ovg_op_attention(const void* qkv, void* output, int64_t rows,
       ovg::Require(first >= 0 && length >= 1 && first + length <= rows,
                    "sequence outside the rows");
       ovg::Require(first % ovg::kSequenceAlign == 0,
-                   "sequence start must be a multiple of 8");
+                   "sequence start must be a multiple of 16");
       end = std::max(end, first + (length + 31) / 32 * 32);
       for (int64_t q = 0; q < length; q += 32)
         work.push_back({static_cast<int>(first + q),
@@ -200,7 +200,7 @@ int ovg_op_attention(const void* qkv, void* output, int64_t rows,
     // Keys are read in whole 32-row tiles: copy q|k into a buffer padded to
     // the last tile, and V into V^T.
     const int padded = static_cast<int>(std::max(end, rows));
-    const int ldvt = (padded + 7) / 8 * 8;
+    const int ldvt = (padded + 15) / 16 * 16;
     Scratch<ovg::half_t> qk(static_cast<std::size_t>(padded) * ld_qkv);
     Scratch<ovg::half_t> vt(static_cast<std::size_t>(kv_heads) * 128 * ldvt);
     Scratch<ovg::AttentionWork> dwork(work.size());

@@ -187,7 +187,7 @@ __global__ void TransposeVKernel(const half_t* qkv, int ld_qkv, half_t* vt,
   const int g = blockIdx.z;
   if (row >= rows)
     return;
-  vt[static_cast<size_t>(g * 128 + d) * ldvt + row] =
+  vt[static_cast<size_t>(g * 128 + d) * ldvt + VtColumn(row)] =
       qkv[static_cast<size_t>(row) * ld_qkv + (heads + kv_heads + g) * 128 + d];
 }
 

@@ -173,8 +173,8 @@ class Engine {
     Require(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0,
             "heads must be a positive multiple of kv_heads");
     const std::int64_t group = c.heads / c.kv_heads;
-    Require(group == 1 || group == 2 || group == 4,
-            "query heads per kv head must be 1, 2 or 4");
+    Require(group == 1 || group == 2,
+            "query heads per kv head must be 1 or 2");
     Require(c.hidden_size % 64 == 0 && c.hidden_size <= 4096,
             "hidden_size must be a multiple of 64 and at most 4096");
     Require(c.intermediate_size % 64 == 0,
@@ -514,7 +514,7 @@ std::int64_t Engine::DeviceBytes() const {
 // more inputs: per item the conditional sequence (text, reference frames,
 // target frames; positions 0 .. length - 1) and the unconditional sequence
 // (its target frames only; positions 0 .. frames - 1), each starting on a
-// multiple of 8 rows.
+// multiple of 16 rows.
 Layout Engine::Plan(const std::vector<Input>& inputs) const {
   Require(!inputs.empty(), "no input");
   const std::int64_t C = cfg_.audio_codebooks;
@@ -619,7 +619,7 @@ void Engine::Prepare(const Layout& L) {
       static_cast<std::size_t>(cfg_.heads + cfg_.kv_heads) * 128;
   const std::size_t width =
       static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
-  const int ldvt = (L.rows_alloc + 7) / 8 * 8;
+  const int ldvt = (L.rows_alloc + 15) / 16 * 16;
   Grow(ids_, C * ra);
   Grow(row_kind_, ra);
   Grow(positions_, ra);
@@ -683,7 +683,7 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
   const int qk_width = static_cast<int>(cfg_.heads + cfg_.kv_heads) * 128;
   const int qkv_n = qk_width + static_cast<int>(cfg_.kv_heads) * 128;
   const int heads_width = static_cast<int>(cfg_.heads) * 128;
-  const int ldvt = (L.rows_alloc + 7) / 8 * 8;
+  const int ldvt = (L.rows_alloc + 15) / 16 * 16;
   const double R = L.real_rows;
   const int C = static_cast<int>(cfg_.audio_codebooks);
   const int Vw = static_cast<int>(cfg_.audio_codebooks * cfg_.audio_vocab_size);

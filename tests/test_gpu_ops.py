@@ -154,8 +154,8 @@ def test_rmsnorm_matches_oracle():
 
 # ------------------------------------------------------------------ attention
 
-@pytest.mark.parametrize("seqs", [[(0, 330), (336, 250)], [(0, 1), (8, 31)],
-                                  [(0, 680), (680, 375)], [(0, 33)]])
+@pytest.mark.parametrize("seqs", [[(0, 330), (336, 250)], [(0, 1), (16, 31)],
+                                  [(0, 680), (688, 375)], [(0, 33)]])
 def test_attention_matches_oracle(seqs):
     rng = np.random.default_rng(len(seqs) + seqs[-1][1])
     heads, kv = 16, 8

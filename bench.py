@@ -84,6 +84,10 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=2,
                     help="unmasking steps timed for the CPU baseline (0 skips it)")
     ap.add_argument("--profile-repeats", type=int, default=3)
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only copy this many MiB device to device 3 times (a "
+                         "copy kernel of known size for calibrating memory "
+                         "counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -91,9 +95,18 @@ def main():
         sys.exit(2)
 
     import torch
-    import omnivoice_amd as ov
     if not torch.cuda.is_available():
         raise SystemExit("no GPU visible")
+    if args.copy_calibration_mb > 0:
+        n = args.copy_calibration_mb << 20
+        src = torch.full((n,), 1, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "copies": 3}), flush=True)
+        return
+    import omnivoice_amd as ov
 
     cfg = ov.released_config()
     text, reference, target = WORKLOADS[args.workload]
@@ -144,6 +157,15 @@ def main():
                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                     "traffic": None, "kernel": dominant,
                     "avg_launch_us": per_launch_ms * 1e3}
+    # HBM bytes per launch of the dominant kernel, from the calibrated
+    # FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/.
+    traffic_path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    if os.path.exists(traffic_path):
+        with open(traffic_path) as f:
+            measured = json.load(f).get(dominant)
+        if measured:
+            roofline["traffic"] = measured["bytes"]
+            roofline["traffic_source"] = "profiles/" + measured["source"]
     gemm_ms = sum(s["total_ms"] for n, s in stats.items() if n.startswith("gemm_")
                   and n != "gemm_audio_heads")
     gemm_flops = sum(s["flops"] for n, s in stats.items() if n.startswith("gemm_")

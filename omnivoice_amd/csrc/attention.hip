@@ -351,10 +351,12 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   const dim3 grid(p.work_count * p.kv_heads);
   switch (group) {
     case 1:
-      AttentionKernel<1><<<grid, dim3(5 * 64), AttentionLds<1>(), stream>>>(p);
+      Dispatch(AttentionKernel<1>, grid, dim3(5 * 64), AttentionLds<1>(), stream,
+               true, true, p);
       break;
     case 2:
-      AttentionKernel<2><<<grid, dim3(9 * 64), AttentionLds<2>(), stream>>>(p);
+      Dispatch(AttentionKernel<2>, grid, dim3(9 * 64), AttentionLds<2>(), stream,
+               true, true, p);
       break;
     default:
       throw Error("attention: query heads per kv head must be 1 or 2");

@@ -280,8 +280,8 @@ void LaunchScore(const ScoreParams& p, hipStream_t stream) {
   Require(p.item_count >= 1 && p.max_frames >= 1, "score: no frames");
   const int waves = p.max_frames * p.codebooks;
   const dim3 grid((waves + kScoreWaves - 1) / kScoreWaves, p.item_count);
-  hipLaunchKernelGGL(ScoreKernel, grid, dim3(kScoreWaves * kWave), 0, stream,
-                     p);
+  Dispatch(ScoreKernel, grid, dim3(kScoreWaves * kWave), 0, stream, true, true,
+           p);
   Check(hipGetLastError(), "score launch");
 }
 
@@ -289,8 +289,8 @@ void LaunchSelect(const SelectParams& p, int max_total, hipStream_t stream) {
   Require(max_total >= 1 && max_total <= kSelectThreads * kSelectPerThread,
           "select: codebooks * frames outside [1, 16384]");
   Require(p.item_count >= 1, "select: no items");
-  hipLaunchKernelGGL(SelectKernel, dim3(p.item_count), dim3(kSelectThreads),
-                     0, stream, p);
+  Dispatch(SelectKernel, dim3(p.item_count), dim3(kSelectThreads), 0, stream,
+           true, true, p);
   Check(hipGetLastError(), "select launch");
 }
 

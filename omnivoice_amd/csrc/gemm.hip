@@ -47,22 +47,34 @@ namespace {
 constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 64;
-constexpr int kThreads = 512;
 constexpr int kXcds = 8;
 constexpr int kABytes = kBM * kBK * 2;  // one stage of A: 16 KB
 constexpr int kBBytes = kBN * kBK * 2;
 constexpr int kStageBytes = kABytes + kBBytes;
-constexpr int kAInstr = kABytes / 1024 / 8;  // 1 KB DMA blocks per wave
-constexpr int kBInstr = kBBytes / 1024 / 8;
-constexpr int kLoads = kAInstr + kBInstr;  // DMA instructions per stage
 constexpr int kTileFloats = kBM * kBN;
-// The accumulator swap: each wave hands over 8 x 16 bytes per lane.
-constexpr int kSwapBytes = kThreads * 8 * 16;
 
-template <int STAGES>
+// FM = 32-row MFMA blocks per wave strip: 8 waves of 32 x 128 strips (FM 1)
+// or 4 waves of 64 x 128 strips (FM 2, a quarter less LDS read traffic per
+// MFMA). Both split each K step between two groups of waves.
+template <int FM>
+struct Shape {
+  static constexpr int kWaves = 8 / FM;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kStrips = kWaves / 2;
+  static constexpr int kOwned = 8 * FM;  // owned elements per column block
+  // DMA instructions (1 KB each) per wave per stage, for A and for B.
+  static constexpr int kAInstr = kABytes / 1024 / kWaves;
+  static constexpr int kBInstr = kBBytes / 1024 / kWaves;
+  static constexpr int kLoads = kAInstr + kBInstr;
+  // The accumulator swap: every wave hands over kOwned / 4 x 4 float4 per
+  // lane (64 KB in all).
+  static constexpr int kSwapBytes = kThreads * kOwned * 4 * 4;
+};
+
+template <int STAGES, int FM>
 constexpr int LdsBytes() {
-  return STAGES * kStageBytes > kSwapBytes ? STAGES * kStageBytes
-                                           : kSwapBytes;
+  return STAGES * kStageBytes > Shape<FM>::kSwapBytes ? STAGES * kStageBytes
+                                                      : Shape<FM>::kSwapBytes;
 }
 
 // LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
@@ -115,9 +127,10 @@ __device__ __forceinline__ void StageBarrier() {
 
 // ------------------------------------------------------------- epilogues
 // A wave's owned values: v[c][e] is column 32 c + (lane & 31) of row
-// row0 + RowOf(e), e < 8, where row0 = m0 + 32 wave_m + 16 group.
+// row0 + RowOf(e), e < 8 FM, where row0 = m0 + 32 FM strip + 16 FM group.
+template <int FM>
 struct Owned {
-  float v[4][8];
+  float v[4][8 * FM];
 };
 
 __device__ __forceinline__ int RowOf(int e, int lane) {
@@ -134,9 +147,10 @@ __device__ __forceinline__ float HalfWaveSum(float v) {
   return v + __shfl_xor(v, 16);
 }
 
-__device__ __forceinline__ void StoreOwned(const GemmParams& p, const Owned& o,
-                                           float* y, int row0, int n0,
-                                           bool accumulate) {
+template <int FM>
+__device__ __forceinline__ void StoreOwned(const GemmParams& p,
+                                           const Owned<FM>& o, float* y,
+                                           int row0, int n0, bool accumulate) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -144,7 +158,7 @@ __device__ __forceinline__ void StoreOwned(const GemmParams& p, const Owned& o,
     if (n >= p.n)
       continue;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < 8 * FM; ++e) {
       const int m = row0 + RowOf(e, lane);
       if (m < p.m) {
         float* dst = y + static_cast<size_t>(m) * p.ldc + n;
@@ -154,8 +168,10 @@ __device__ __forceinline__ void StoreOwned(const GemmParams& p, const Owned& o,
   }
 }
 
-__device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
-                                         int row0, int slot) {
+template <int FM>
+__device__ __forceinline__ void QkvOwned(const GemmParams& p,
+                                         const Owned<FM>& o, int row0,
+                                         int slot) {
   const int lane = threadIdx.x & 63;
   const int j = lane & 31;
   if (slot < p.heads + p.kv_heads) {
@@ -165,18 +181,18 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
     for (int c = 0; c < 4; ++c)
       w[c] = weight[32 * c + j];
     // Issue every position and rotary load before the arithmetic.
-    int position[8];
+    int position[8 * FM];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8 * FM; ++e)
       position[e] = p.positions[min(row0 + RowOf(e, lane), p.m - 1)];
-    float2 cs[8][2];
+    float2 cs[8 * FM][2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8 * FM; ++e)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         cs[e][c] = p.rope[static_cast<size_t>(position[e]) * 64 + 32 * c + j];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < 8 * FM; ++e) {
       const int m = row0 + RowOf(e, lane);
       float squares = o.v[0][e] * o.v[0][e];
 #pragma unroll
@@ -206,7 +222,7 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
   for (int c = 0; c < 4; ++c) {
     half_t* out = p.vt + static_cast<size_t>(g * 128 + 32 * c + j) * p.ldvt;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 2 * FM; ++h) {
       const int m = row0 + RowOf(4 * h, lane);
       const half4 v = {static_cast<half_t>(o.v[c][4 * h]),
                        static_cast<half_t>(o.v[c][4 * h + 1]),
@@ -222,12 +238,13 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p, const Owned& o,
   }
 }
 
+template <int FM>
 __device__ __forceinline__ void SwiGluOwned(const GemmParams& p,
-                                            const Owned& o, int row0,
+                                            const Owned<FM>& o, int row0,
                                             int tile_n) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < 8 * FM; ++e) {
     const int m = row0 + RowOf(e, lane);
     if (m >= p.m)
       continue;
@@ -241,9 +258,9 @@ __device__ __forceinline__ void SwiGluOwned(const GemmParams& p,
   }
 }
 
-template <Epilogue EPI>
+template <Epilogue EPI, int FM>
 __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
-                                              const Owned& o, int row0,
+                                              const Owned<FM>& o, int row0,
                                               int tile_n) {
   if constexpr (EPI == Epilogue::kStore)
     StoreOwned(p, o, p.y, row0, tile_n * kBN, false);
@@ -257,9 +274,10 @@ __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
 
 // ------------------------------------------------------------- main kernel
 
-template <int STAGES, Epilogue EPI>
-__global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
-                                                       int tiles_m) {
+template <int STAGES, Epilogue EPI, int FM>
+__global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
+    GemmParams p, int tiles_m) {
+  using S = Shape<FM>;
   extern __shared__ __align__(16) unsigned char lds[];
 
   // XCD-aware remap of the dispatch order, then M-fastest tile order.
@@ -285,23 +303,23 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
   const int lane = tid & 63;
   // Wave-uniform, so that everything derived from it stays scalar.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int group = wave >> 2;  // K substeps 2 group, 2 group + 1
-  const int wave_m = wave & 3;  // rows 32 wave_m .. 32 wave_m + 31
+  const int group = wave / S::kStrips;  // K substeps 2 group, 2 group + 1
+  const int strip = wave % S::kStrips;  // rows 32 FM strip .. + 32 FM - 1
 
   // DMA sources: wave w fills 1 KB blocks w * kAInstr + i of A (8 rows each)
   // and of B; lane l brings row 8 b + l / 8 at LDS position l % 8, i.e.
   // chunk Swizzle(row, l % 8). Rows past M or N read the last valid row
   // (their results are never stored).
-  uint32_t a_src[kAInstr], b_src[kBInstr];  // byte offsets from the bases
+  uint32_t a_src[S::kAInstr], b_src[S::kBInstr];  // byte offsets from bases
 #pragma unroll
-  for (int i = 0; i < kAInstr; ++i) {
-    const int row = (wave * kAInstr + i) * 8 + (lane >> 3);
+  for (int i = 0; i < S::kAInstr; ++i) {
+    const int row = (wave * S::kAInstr + i) * 8 + (lane >> 3);
     a_src[i] = static_cast<uint32_t>(min(m0 + row, p.m - 1)) * p.lda * 2 +
                Swizzle(row, lane & 7) * 16;
   }
 #pragma unroll
-  for (int i = 0; i < kBInstr; ++i) {
-    const int row = (wave * kBInstr + i) * 8 + (lane >> 3);
+  for (int i = 0; i < S::kBInstr; ++i) {
+    const int row = (wave * S::kBInstr + i) * 8 + (lane >> 3);
     b_src[i] = static_cast<uint32_t>(min(n0 + row, p.n - 1)) * p.ldb * 2 +
                Swizzle(row, lane & 7) * 16;
   }
@@ -314,27 +332,32 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     const uint32_t base = lds_base + stage * kStageBytes;
     const int kk = kt * kBK * 2;
 #pragma unroll
-    for (int i = 0; i < kAInstr; ++i)
-      DmaToLds(a_base + kk, a_src[i], base + (wave * kAInstr + i) * 1024);
+    for (int i = 0; i < S::kAInstr; ++i)
+      DmaToLds(a_base + kk, a_src[i], base + (wave * S::kAInstr + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < kBInstr; ++i)
+    for (int i = 0; i < S::kBInstr; ++i)
       DmaToLds(b_base + kk, b_src[i],
-               base + kABytes + (wave * kBInstr + i) * 1024);
+               base + kABytes + (wave * S::kBInstr + i) * 1024);
   };
 
-  floatx16 acc[4];
+  floatx16 acc[FM][4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    acc[c] = floatx16{};
+  for (int f = 0; f < FM; ++f)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      acc[f][c] = floatx16{};
 
   // Byte offsets of this lane's fragments inside a stage (stage-invariant):
   // A rows of the wave's strip, B rows 32 c + (lane & 31) for column block c.
-  int a_off[2], b_off[2][4];
+  int a_off[2][FM], b_off[2][4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int chunk = 2 * (2 * group + j) + (lane >> 5);
-    const int ra = wave_m * 32 + (lane & 31);
-    a_off[j] = ra * 128 + Swizzle(ra, chunk) * 16;
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+      const int ra = (strip * FM + f) * 32 + (lane & 31);
+      a_off[j][f] = ra * 128 + Swizzle(ra, chunk) * 16;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int rb = c * 32 + (lane & 31);
@@ -342,14 +365,16 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     }
   }
   struct Fragments {
-    half8 a[2], b[2][4];
+    half8 a[2][FM], b[2][4];
   };
   auto read = [&](int kt) {
     const unsigned char* s = lds + (kt % STAGES) * kStageBytes;
     Fragments fr;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      fr.a[j] = *reinterpret_cast<const half8*>(s + a_off[j]);
+#pragma unroll
+      for (int f = 0; f < FM; ++f)
+        fr.a[j][f] = *reinterpret_cast<const half8*>(s + a_off[j][f]);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         fr.b[j][c] = *reinterpret_cast<const half8*>(s + b_off[j][c]);
@@ -369,11 +394,11 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
   {
     const int ahead = min(STAGES, steps) - 1;  // stages after 0 in flight
     if (ahead >= 3)
-      WaitLoads<3 * kLoads>();
+      WaitLoads<3 * S::kLoads>();
     else if (ahead == 2)
-      WaitLoads<2 * kLoads>();
+      WaitLoads<2 * S::kLoads>();
     else if (ahead == 1)
-      WaitLoads<kLoads>();
+      WaitLoads<S::kLoads>();
     else
       WaitLoads<0>();
   }
@@ -386,9 +411,9 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     const int ahead = min(STAGES - 2, steps - 2 - kt);
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     if (ahead >= 2)
-      WaitLoads<2 * kLoads>();
+      WaitLoads<2 * S::kLoads>();
     else if (ahead == 1)
-      WaitLoads<kLoads>();
+      WaitLoads<S::kLoads>();
     else
       WaitLoads<0>();
     StageBarrier();
@@ -402,8 +427,10 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        acc[c] = Mfma32(fr.a[j], fr.b[j][c], acc[c]);
+      for (int f = 0; f < FM; ++f)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[f][c] = Mfma32(fr.a[j][f], fr.b[j][c], acc[f][c]);
     __builtin_amdgcn_sched_barrier(0);
   };
   // Two fragment sets in ping-pong, so that a step's MFMAs never wait for
@@ -429,109 +456,137 @@ __global__ __launch_bounds__(kThreads) void GemmKernel(GemmParams p,
     mma(even);
   }
 
-  // Swap accumulator halves: group g keeps elements 8 g .. 8 g + 7 (rows
-  // 16 g .. 16 g + 15 of the strip) and hands the other eight to its partner
-  // wave ^ 4, as float4 q = 2 c + h at ((wave * 8 + q) * 64 + lane) * 16.
+  // Swap accumulator halves. Flattening a column block's accumulators as
+  // e = 16 f + r, group g keeps e in [8 FM g, 8 FM (g + 1)) (rows
+  // 16 FM g .. 16 FM g + 16 FM - 1 of the strip) and hands the rest to its
+  // partner wave (same strip, other group) as float4 number q = 2 FM c + h
+  // at float4 index (wave * 8 FM + q) * 64 + lane.
   asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
   StageBarrier();
+  // Element e of column block c: accumulator e / 16, register e % 16. The
+  // indices below are compile-time after unrolling; the group only selects
+  // between two of them, so the accumulators stay in registers.
+#define OVG_ACC(c, e) acc[(e) >> 4][c][(e) & 15]
+  constexpr int kQuads = 2 * FM;  // float4 per column block
+  constexpr int kHalf = 8 * FM;   // elements per group and column block
+  const bool upper = group == 1;
   {
-    floatx4* mine = reinterpret_cast<floatx4*>(lds) + wave * 8 * 64 + lane;
-    const int give = 8 * (1 - group);
+    floatx4* mine = reinterpret_cast<floatx4*>(lds) + wave * 4 * kQuads * 64 + lane;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        mine[(2 * c + h) * 64] = floatx4{acc[c][give + 4 * h],
-                                         acc[c][give + 4 * h + 1],
-                                         acc[c][give + 4 * h + 2],
-                                         acc[c][give + 4 * h + 3]};
-  }
-  __syncthreads();
-  Owned own;
-  {
-    const floatx4* theirs =
-        reinterpret_cast<const floatx4*>(lds) + (wave ^ 4) * 8 * 64 + lane;
-    const int keep = 8 * group;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const floatx4 t = theirs[(2 * c + h) * 64];
+      for (int h = 0; h < kQuads; ++h) {
+        floatx4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          own.v[c][4 * h + i] = acc[c][keep + 4 * h + i] + t[i];
+          v[i] = upper ? OVG_ACC(c, 4 * h + i) : OVG_ACC(c, kHalf + 4 * h + i);
+        mine[(kQuads * c + h) * 64] = v;
       }
   }
-  const int row0 = m0 + 32 * wave_m + 16 * group;
+  __syncthreads();
+  Owned<FM> own;
+  {
+    const int partner = (1 - group) * S::kStrips + strip;
+    const floatx4* theirs =
+        reinterpret_cast<const floatx4*>(lds) + partner * 4 * kQuads * 64 + lane;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int h = 0; h < kQuads; ++h) {
+        const floatx4 t = theirs[(kQuads * c + h) * 64];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          own.v[c][4 * h + i] =
+              (upper ? OVG_ACC(c, kHalf + 4 * h + i) : OVG_ACC(c, 4 * h + i)) + t[i];
+      }
+  }
+#undef OVG_ACC
+  const int row0 = m0 + 32 * FM * strip + 16 * FM * group;
 
   if constexpr (EPI == Epilogue::kPartial) {
     // Each split owns a full [M][ldc] slice; the row kernel that consumes
     // the GEMM adds the slices.
-    StoreOwned(p, own, p.y + static_cast<size_t>(split) * p.split_stride,
-               row0, n0, false);
+    StoreOwned<FM>(p, own, p.y + static_cast<size_t>(split) * p.split_stride,
+                   row0, n0, false);
     return;
   }
   if (p.splits > 1) {
     floatx4* mine = reinterpret_cast<floatx4*>(p.partials) +
-                    ((static_cast<size_t>(tile) * p.splits + split) * 8 + wave) * 8 * 64 +
+                    ((static_cast<size_t>(tile) * p.splits + split) * S::kWaves + wave) *
+                        4 * kQuads * 64 +
                     lane;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        mine[(2 * c + h) * 64] = floatx4{own.v[c][4 * h], own.v[c][4 * h + 1],
-                                         own.v[c][4 * h + 2], own.v[c][4 * h + 3]};
+      for (int h = 0; h < kQuads; ++h)
+        mine[(kQuads * c + h) * 64] =
+            floatx4{own.v[c][4 * h], own.v[c][4 * h + 1], own.v[c][4 * h + 2],
+                    own.v[c][4 * h + 3]};
     return;
   }
-  OwnedEpilogue<EPI>(p, own, row0, tile_n);
+  OwnedEpilogue<EPI, FM>(p, own, row0, tile_n);
 }
 
 // Sums a tile's split-K partials in split order 0, 1, ... (a fixed order,
 // reproducible bit for bit) in the same per-wave layout the GEMM kernel
 // stored them in, and applies the epilogue.
-template <Epilogue EPI>
-__global__ __launch_bounds__(kThreads) void SplitReduceKernel(GemmParams p,
-                                                              int tiles_m) {
+template <Epilogue EPI, int FM>
+__global__ __launch_bounds__(Shape<FM>::kThreads) void SplitReduceKernel(
+    GemmParams p, int tiles_m) {
+  using S = Shape<FM>;
+  constexpr int kQuads = 2 * FM;
   const int tile = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const size_t split_stride = static_cast<size_t>(S::kWaves) * 4 * kQuads * 64;
   const floatx4* base = reinterpret_cast<const floatx4*>(p.partials) +
-                        (static_cast<size_t>(tile) * p.splits * 8 + wave) * 8 * 64 +
-                        lane;
-  Owned own;
+                        static_cast<size_t>(tile) * p.splits * split_stride +
+                        wave * 4 * kQuads * 64 + lane;
+  Owned<FM> own;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < 4 * kQuads; ++q) {
     floatx4 sum = base[q * 64];
     for (int s = 1; s < p.splits; ++s)
-      sum += base[static_cast<size_t>(s) * 8 * 8 * 64 + q * 64];
+      sum += base[s * split_stride + q * 64];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      own.v[q >> 1][4 * (q & 1) + i] = sum[i];
+      own.v[q / kQuads][4 * (q % kQuads) + i] = sum[i];
   }
   const int tile_m = tile % tiles_m;
-  const int row0 = tile_m * kBM + 32 * (wave & 3) + 16 * (wave >> 2);
-  OwnedEpilogue<EPI>(p, own, row0, tile / tiles_m);
+  const int row0 = tile_m * kBM + 32 * FM * (wave % S::kStrips) +
+                   16 * FM * (wave / S::kStrips);
+  OwnedEpilogue<EPI, FM>(p, own, row0, tile / tiles_m);
 }
 
-template <int STAGES, Epilogue EPI>
+template <int STAGES, Epilogue EPI, int FM>
 void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
-  GemmKernel<STAGES, EPI>
-      <<<dim3(groups), dim3(kThreads), LdsBytes<STAGES>(), stream>>>(p, tiles_m);
-  if (p.splits > 1 && EPI != Epilogue::kPartial)
-    SplitReduceKernel<EPI><<<dim3(groups / p.splits), dim3(kThreads), 0,
-                             stream>>>(p, tiles_m);
+  const bool reduce = p.splits > 1 && EPI != Epilogue::kPartial;
+  Dispatch(GemmKernel<STAGES, EPI, FM>, dim3(groups), dim3(Shape<FM>::kThreads),
+           LdsBytes<STAGES, FM>(), stream, true, !reduce, p, tiles_m);
+  if (reduce)
+    Dispatch(SplitReduceKernel<EPI, FM>, dim3(groups / p.splits),
+             dim3(Shape<FM>::kThreads), 0, stream, false, true, p, tiles_m);
+}
+
+template <Epilogue EPI, int FM>
+void LaunchStages(const GemmParams& p, const GemmPlan& plan, int tiles_m,
+                  int groups, hipStream_t stream) {
+  if (plan.stages == 2)
+    Launch<2, EPI, FM>(p, tiles_m, groups, stream);
+  else if (plan.stages == 4)
+    Launch<4, EPI, FM>(p, tiles_m, groups, stream);
+  else
+    Launch<3, EPI, FM>(p, tiles_m, groups, stream);
 }
 
 template <Epilogue EPI>
 void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
   const int tiles_m = (p.m + kBM - 1) / kBM;
   const int groups = plan.tiles * plan.splits;
-  if (plan.stages == 2)
-    Launch<2, EPI>(p, tiles_m, groups, stream);
-  else if (plan.stages == 4)
-    Launch<4, EPI>(p, tiles_m, groups, stream);
-  else
-    Launch<3, EPI>(p, tiles_m, groups, stream);
+  // 32-row strips (8 waves) measured faster than 64-row strips (4 waves,
+  // one per SIMD) at every generator shape, despite the latter's lower LDS
+  // traffic per MFMA.
+  LaunchStages<EPI, 1>(p, plan, tiles_m, groups, stream);
 }
 
 }  // namespace

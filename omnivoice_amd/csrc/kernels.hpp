@@ -4,6 +4,7 @@
 #ifndef OMNIVOICE_AMD_KERNELS_HPP_
 #define OMNIVOICE_AMD_KERNELS_HPP_
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -27,6 +28,32 @@ inline void Check(hipError_t status, const char* what) {
 inline void Require(bool condition, const std::string& what) {
   if (!condition)
     throw Error(what);
+}
+
+// Kernel-accurate timing for the profiler: while set on the launching
+// thread, a launcher dispatches its first kernel with `start` and its last
+// with `stop` (hipExtLaunchKernel), so the events bracket the kernels
+// themselves rather than the gaps between dispatches. Null otherwise.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+inline LaunchTiming& CurrentTiming() {
+  static thread_local LaunchTiming timing;
+  return timing;
+}
+
+template <typename... Params, typename... Args>
+void Dispatch(void (*kernel)(Params...), dim3 grid, dim3 block,
+              std::uint32_t lds_bytes, hipStream_t stream, bool first,
+              bool last, Args... args) {
+  const LaunchTiming& t = CurrentTiming();
+  hipEvent_t start = first ? t.start : nullptr;
+  hipEvent_t stop = last ? t.stop : nullptr;
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, start, stop,
+                          0, static_cast<Params>(args)...);
+  else
+    kernel<<<grid, block, lds_bytes, stream>>>(static_cast<Params>(args)...);
 }
 
 // ---------------------------------------------------------------- GEMM

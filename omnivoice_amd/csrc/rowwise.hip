@@ -203,8 +203,8 @@ void LaunchEmbed(const EmbedParams& p, hipStream_t stream) {
   Require(p.rows > 0, "embed: no rows");
   Require(p.hidden_size % 4 == 0 && p.hidden_size <= 4 * 4 * kRowThreads,
           "embed: hidden size must be a multiple of 4 and at most 4096");
-  hipLaunchKernelGGL(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream,
-                     p);
+  Dispatch(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream, true, true,
+           p);
   Check(hipGetLastError(), "embed launch");
 }
 
@@ -216,11 +216,11 @@ void LaunchRmsNorm(const float* x, const int* gather, const float* w,
           "rmsnorm: width must be a multiple of 4 and at most 4096");
   const dim3 grid((rows + kRowThreads / 64 - 1) / (kRowThreads / 64));
   if (width <= 1024)
-    RmsNormKernel<4><<<grid, kRowThreads, 0, stream>>>(x, gather, w, out, rows,
-                                                       width, eps);
+    Dispatch(RmsNormKernel<4>, grid, dim3(kRowThreads), 0, stream, true, true,
+             x, gather, w, out, rows, width, eps);
   else
-    RmsNormKernel<16><<<grid, kRowThreads, 0, stream>>>(x, gather, w, out,
-                                                        rows, width, eps);
+    Dispatch(RmsNormKernel<16>, grid, dim3(kRowThreads), 0, stream, true,
+             true, x, gather, w, out, rows, width, eps);
   Check(hipGetLastError(), "rmsnorm launch");
 }
 
@@ -231,9 +231,11 @@ void LaunchAddNorm(const AddNormParams& p, hipStream_t stream) {
   Require(p.splits >= 1 && p.splits <= 8, "addnorm: 1 to 8 partial slices");
   const dim3 grid((p.rows + kRowThreads / 64 - 1) / (kRowThreads / 64));
   if (p.splits <= 4)
-    AddNormKernel<4, 4><<<grid, kRowThreads, 0, stream>>>(p);
+    Dispatch(AddNormKernel<4, 4>, grid, dim3(kRowThreads), 0, stream, true,
+             true, p);
   else
-    AddNormKernel<4, 8><<<grid, kRowThreads, 0, stream>>>(p);
+    Dispatch(AddNormKernel<4, 8>, grid, dim3(kRowThreads), 0, stream, true,
+             true, p);
   Check(hipGetLastError(), "addnorm launch");
 }
 
@@ -241,16 +243,16 @@ void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
                       int rows, int heads, int kv_heads, hipStream_t stream) {
   Require(rows > 0 && ldvt >= rows, "transpose: bad rows");
   const dim3 grid((rows + 255) / 256, 128, kv_heads);
-  hipLaunchKernelGGL(TransposeVKernel, grid, dim3(256), 0, stream, qkv,
-                     ld_qkv, vt, ldvt, rows, heads, kv_heads);
+  Dispatch(TransposeVKernel, grid, dim3(256), 0, stream, true, true, qkv,
+           ld_qkv, vt, ldvt, rows, heads, kv_heads);
   Check(hipGetLastError(), "transpose launch");
 }
 
 void LaunchFill(int* data, int value, int count, hipStream_t stream) {
   if (count <= 0)
     return;
-  hipLaunchKernelGGL(FillKernel, dim3((count + 255) / 256), dim3(256), 0,
-                     stream, data, value, count);
+  Dispatch(FillKernel, dim3((count + 255) / 256), dim3(256), 0, stream, true,
+           true, data, value, count);
   Check(hipGetLastError(), "fill launch");
 }
 

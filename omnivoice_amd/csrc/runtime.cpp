@@ -131,9 +131,15 @@ class Profiler {
     e.bytes = bytes;
     Check(hipEventCreate(&e.begin), "hipEventCreate");
     Check(hipEventCreate(&e.end), "hipEventCreate");
-    Check(hipEventRecord(e.begin, stream_), "hipEventRecord");
-    launch();
-    Check(hipEventRecord(e.end, stream_), "hipEventRecord");
+    // The launcher's kernels record the events themselves (CurrentTiming).
+    CurrentTiming() = LaunchTiming{e.begin, e.end};
+    try {
+      launch();
+    } catch (...) {
+      CurrentTiming() = LaunchTiming{};
+      throw;
+    }
+    CurrentTiming() = LaunchTiming{};
     entries_.push_back(e);
   }
   void Collect(std::map<std::string, KernelStat>* stats) {

@@ -39,25 +39,37 @@ __global__ __launch_bounds__(kRowThreads) void EmbedKernel(EmbedParams p) {
   half_t* normed = p.normed + static_cast<size_t>(row) * p.hidden_size;
   float squares = 0.0F;
   constexpr int kMaxChunks = 4;  // hidden <= 4096
-  floatx4 v[kMaxChunks];
+  constexpr int kMaxCodebooks = 16;
+  // The row's ids, then every embedding row and the norm weights, are
+  // loaded before any arithmetic: two dependent memory round trips in all.
+  int entry[kMaxCodebooks];
+  const int codebooks = kind == 1 ? p.codebooks : (kind == 0 ? 1 : 0);
+#pragma unroll
+  for (int c = 0; c < kMaxCodebooks; ++c)
+    entry[c] = c >= codebooks ? 0
+               : kind == 0    ? p.ids[row]
+                              : c * p.vocab + p.ids[static_cast<size_t>(c) * p.ld_ids + row];
+  const float* table = kind == 0 ? p.text : p.audio;
+  floatx4 v[kMaxChunks], w[kMaxChunks];
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {
     const int d = (threadIdx.x + i * kRowThreads) * 4;
     v[i] = floatx4{0, 0, 0, 0};
+    w[i] = floatx4{0, 0, 0, 0};
     if (d >= p.hidden_size)
       continue;
-    if (kind == 0) {
-      const int id = p.ids[row];
-      v[i] = *reinterpret_cast<const floatx4*>(
-          p.text + static_cast<size_t>(id) * p.hidden_size + d);
-    } else if (kind == 1) {
-      for (int c = 0; c < p.codebooks; ++c) {
-        const size_t entry = static_cast<size_t>(c) * p.vocab +
-                             p.ids[static_cast<size_t>(c) * p.ld_ids + row];
+    w[i] = *reinterpret_cast<const floatx4*>(p.norm + d);
+#pragma unroll
+    for (int c = 0; c < kMaxCodebooks; ++c)
+      if (c < codebooks)
         v[i] += *reinterpret_cast<const floatx4*>(
-            p.audio + entry * p.hidden_size + d);
-      }
-    }
+            table + static_cast<size_t>(entry[c]) * p.hidden_size + d);
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int d = (threadIdx.x + i * kRowThreads) * 4;
+    if (d >= p.hidden_size)
+      continue;
     *reinterpret_cast<floatx4*>(out + d) = v[i];
     squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
                v[i][3] * v[i][3];
@@ -70,11 +82,10 @@ __global__ __launch_bounds__(kRowThreads) void EmbedKernel(EmbedParams p) {
     const int d = (threadIdx.x + i * kRowThreads) * 4;
     if (d >= p.hidden_size)
       continue;
-    const floatx4 w = *reinterpret_cast<const floatx4*>(p.norm + d);
-    const half4 h = {static_cast<half_t>(w[0] * (v[i][0] * scale)),
-                     static_cast<half_t>(w[1] * (v[i][1] * scale)),
-                     static_cast<half_t>(w[2] * (v[i][2] * scale)),
-                     static_cast<half_t>(w[3] * (v[i][3] * scale))};
+    const half4 h = {static_cast<half_t>(w[i][0] * (v[i][0] * scale)),
+                     static_cast<half_t>(w[i][1] * (v[i][1] * scale)),
+                     static_cast<half_t>(w[i][2] * (v[i][2] * scale)),
+                     static_cast<half_t>(w[i][3] * (v[i][3] * scale))};
     *reinterpret_cast<half4*>(normed + d) = h;
   }
 }
@@ -93,16 +104,20 @@ __global__ __launch_bounds__(kRowThreads) void RmsNormKernel(
     return;
   const int src = gather != nullptr ? gather[r] : r;
   const float* in = x + static_cast<size_t>(src) * width;
-  floatx4 v[CHUNKS];
+  floatx4 v[CHUNKS], wv[CHUNKS];
   float squares = 0.0F;
 #pragma unroll
   for (int i = 0; i < CHUNKS; ++i) {
     const int d = (lane + 64 * i) * 4;
     v[i] = d < width ? *reinterpret_cast<const floatx4*>(in + d)
                      : floatx4{0, 0, 0, 0};
+    wv[i] = d < width ? *reinterpret_cast<const floatx4*>(w + d)
+                      : floatx4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int i = 0; i < CHUNKS; ++i)
     squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
                v[i][3] * v[i][3];
-  }
   const float scale = rsqrtf(WaveSumFast(squares) / static_cast<float>(width) + eps);
   half_t* o = out + static_cast<size_t>(r) * width;
 #pragma unroll
@@ -110,12 +125,11 @@ __global__ __launch_bounds__(kRowThreads) void RmsNormKernel(
     const int d = (lane + 64 * i) * 4;
     if (d >= width)
       break;
-    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + d);
     *reinterpret_cast<half4*>(o + d) =
-        half4{static_cast<half_t>(wv[0] * (v[i][0] * scale)),
-              static_cast<half_t>(wv[1] * (v[i][1] * scale)),
-              static_cast<half_t>(wv[2] * (v[i][2] * scale)),
-              static_cast<half_t>(wv[3] * (v[i][3] * scale))};
+        half4{static_cast<half_t>(wv[i][0] * (v[i][0] * scale)),
+              static_cast<half_t>(wv[i][1] * (v[i][1] * scale)),
+              static_cast<half_t>(wv[i][2] * (v[i][2] * scale)),
+              static_cast<half_t>(wv[i][3] * (v[i][3] * scale))};
   }
 }
 
@@ -131,13 +145,16 @@ __global__ __launch_bounds__(kRowThreads) void AddNormKernel(AddNormParams p) {
   const int src = p.gather != nullptr ? p.gather[r] : r;
   float* h = p.hidden + static_cast<size_t>(src) * p.width;
   const float* part = p.partials + static_cast<size_t>(src) * p.width;
-  floatx4 v[CHUNKS];
+  floatx4 v[CHUNKS], wv[CHUNKS];
   floatx4 parts[MAX_SPLITS][CHUNKS];
+  // Every load (norm weights included) is issued before any arithmetic, so
+  // the row costs one memory round trip.
 #pragma unroll
   for (int i = 0; i < CHUNKS; ++i) {
     const int d = (lane + 64 * i) * 4;
     const bool ok = d < p.width;
     v[i] = ok ? *reinterpret_cast<const floatx4*>(h + d) : floatx4{0, 0, 0, 0};
+    wv[i] = ok ? *reinterpret_cast<const floatx4*>(p.norm + d) : floatx4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < MAX_SPLITS; ++s)
       parts[s][i] = ok && s < p.splits
@@ -170,12 +187,11 @@ __global__ __launch_bounds__(kRowThreads) void AddNormKernel(AddNormParams p) {
     const int d = (lane + 64 * i) * 4;
     if (d >= p.width)
       break;
-    const floatx4 wv = *reinterpret_cast<const floatx4*>(p.norm + d);
     *reinterpret_cast<half4*>(o + d) =
-        half4{static_cast<half_t>(wv[0] * (v[i][0] * scale)),
-              static_cast<half_t>(wv[1] * (v[i][1] * scale)),
-              static_cast<half_t>(wv[2] * (v[i][2] * scale)),
-              static_cast<half_t>(wv[3] * (v[i][3] * scale))};
+        half4{static_cast<half_t>(wv[i][0] * (v[i][0] * scale)),
+              static_cast<half_t>(wv[i][1] * (v[i][1] * scale)),
+              static_cast<half_t>(wv[i][2] * (v[i][2] * scale)),
+              static_cast<half_t>(wv[i][3] * (v[i][3] * scale))};
   }
 }
 
@@ -203,6 +219,7 @@ void LaunchEmbed(const EmbedParams& p, hipStream_t stream) {
   Require(p.rows > 0, "embed: no rows");
   Require(p.hidden_size % 4 == 0 && p.hidden_size <= 4 * 4 * kRowThreads,
           "embed: hidden size must be a multiple of 4 and at most 4096");
+  Require(p.codebooks >= 1 && p.codebooks <= 16, "embed: 1 to 16 codebooks");
   Dispatch(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream, true, true,
            p);
   Check(hipGetLastError(), "embed launch");

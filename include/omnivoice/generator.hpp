@@ -20,9 +20,9 @@ namespace gufo::models::omnivoice {
 
 class Generator {
  public:
-  /// Reference generator.hpp:22-24. An empty `model_root` builds the seeded
-  /// synthetic model (weight seed 1234); loading a checkpoint directory is
-  /// not supported yet and fails with an error.
+  /// Reference generator.hpp:22-24: reads model_root/model.safetensors (the
+  /// checkpoint's float32 tensors). An empty `model_root` builds the seeded
+  /// synthetic model (weight seed 1234) instead.
   [[nodiscard]] static std::unique_ptr<Generator> Load(
       const Config& config, const std::filesystem::path& model_root,
       std::string* error = nullptr);

@@ -107,8 +107,11 @@ typedef struct ovg_kernel_stat {
 /* ---- Load (reference: Generator::Load, generator.hpp:22-24, generator.cpp:364-434) ----
  * `model_root` NULL or "" builds the seeded synthetic model: every matrix and
  * embedding drawn from N(0, 0.02) (the counter-based values of
- * ovg_synthetic_values) and rounded to fp16, norms 1.0. A directory path is
- * not supported yet (returns OVG_ERROR). */
+ * ovg_synthetic_values) and rounded to fp16, norms 1.0. A directory holds
+ * model.safetensors with the checkpoint's float32 tensors under the names of
+ * ovg_host_weights (reference: generator.cpp:377-425); every tensor is found
+ * and checked against `config` before the GPU is touched, and errors name
+ * the file or tensor at fault. `weight_seed` is then unused. */
 int ovg_create(const ovg_config* config, const char* model_root,
                uint64_t weight_seed, ovg_handle** handle, char* error,
                size_t error_len);

@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "../../include/omnivoice_mi355x.h"
+#include "checkpoint.hpp"
 #include "host.hpp"
 #include "kernels.hpp"
 
@@ -1148,15 +1149,53 @@ extern "C" {
 int ovg_create(const ovg_config* config, const char* model_root,
                uint64_t weight_seed, ovg_handle** handle, char* error,
                size_t error_len) {
-  if (model_root != nullptr && model_root[0] != '\0') {
-    SetError(error, error_len,
-             "OmniVoice generator: loading a checkpoint directory is not "
-             "supported yet; pass NULL for the synthetic model or use "
-             "ovg_create_from_host");
-    return OVG_ERROR;
-  }
-  return ovg_create_synthetic(config, weight_seed, 0.0F, handle, error,
-                              error_len);
+  if (model_root == nullptr || model_root[0] == '\0')
+    return ovg_create_synthetic(config, weight_seed, 0.0F, handle, error,
+                                error_len);
+  return Guard("OmniVoice generator: ", error, error_len, [&] {
+    ovg::Require(config != nullptr && handle != nullptr, "null argument");
+    // Every tensor is located and checked against the config before the GPU
+    // is touched (reference: generator.cpp:364-434 reads the same names).
+    const auto file = ovg::SafetensorsFile::Open(std::string(model_root) +
+                                                 "/model.safetensors");
+    const ovg_config& c = *config;
+    const std::int64_t h = c.hidden_size, q_rows = c.heads * c.head_dim,
+                       kv_rows = c.kv_heads * c.head_dim,
+                       audio_rows = c.audio_codebooks * c.audio_vocab_size;
+    ovg::Require(c.layers >= 1, "empty model");
+    std::vector<const float*> layers(
+        static_cast<std::size_t>(c.layers) * OVG_LAYER_TENSORS);
+    for (std::int64_t l = 0; l < c.layers; ++l) {
+      const std::string prefix = "llm.layers." + std::to_string(l) + ".";
+      const float** t = layers.data() + l * OVG_LAYER_TENSORS;
+      t[OVG_LAYER_Q_PROJ] = file->F32(prefix + "self_attn.q_proj.weight", {q_rows, h});
+      t[OVG_LAYER_K_PROJ] = file->F32(prefix + "self_attn.k_proj.weight", {kv_rows, h});
+      t[OVG_LAYER_V_PROJ] = file->F32(prefix + "self_attn.v_proj.weight", {kv_rows, h});
+      t[OVG_LAYER_O_PROJ] = file->F32(prefix + "self_attn.o_proj.weight", {h, q_rows});
+      t[OVG_LAYER_GATE_PROJ] =
+          file->F32(prefix + "mlp.gate_proj.weight", {c.intermediate_size, h});
+      t[OVG_LAYER_UP_PROJ] =
+          file->F32(prefix + "mlp.up_proj.weight", {c.intermediate_size, h});
+      t[OVG_LAYER_DOWN_PROJ] =
+          file->F32(prefix + "mlp.down_proj.weight", {h, c.intermediate_size});
+      t[OVG_LAYER_INPUT_NORM] = file->F32(prefix + "input_layernorm.weight", {h});
+      t[OVG_LAYER_POST_NORM] =
+          file->F32(prefix + "post_attention_layernorm.weight", {h});
+      t[OVG_LAYER_Q_NORM] = file->F32(prefix + "self_attn.q_norm.weight", {c.head_dim});
+      t[OVG_LAYER_K_NORM] = file->F32(prefix + "self_attn.k_norm.weight", {c.head_dim});
+    }
+    ovg_host_weights w{};
+    w.text_embeddings = file->F32("llm.embed_tokens.weight", {c.vocab_size, h});
+    w.audio_embeddings = file->F32("audio_embeddings.weight", {audio_rows, h});
+    w.audio_heads = file->F32("audio_heads.weight", {audio_rows, h});
+    w.final_norm = file->F32("llm.norm.weight", {h});
+    w.layers = layers.data();
+    auto created = std::make_unique<ovg_handle>();
+    created->engine = std::make_unique<ovg::Engine>(c);
+    created->engine->LoadHost(w);
+    *handle = created.release();
+    return OVG_OK;
+  });
 }
 
 int ovg_create_synthetic(const ovg_config* config, uint64_t weight_seed,

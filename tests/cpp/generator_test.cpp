@@ -118,7 +118,7 @@ int main() {
          "malformed input is an error with the generation prefix");
   Expect(!ov::Generator::Load(config, "/nonexistent/checkpoint", &error) &&
              error.rfind("OmniVoice generator: ", 0) == 0,
-         "a checkpoint directory is refused with the generator prefix");
+         "a missing checkpoint is an error with the generator prefix");
 
   std::cout << (failures == 0 ? "ok" : "FAIL") << " generator: " << failures
             << " failures\n";

@@ -70,7 +70,7 @@ def test_bad_config_is_rejected_with_reference_prefix():
     assert str(e.value) == "OmniVoice generator: head_dim must be 128"
 
 
-def test_checkpoint_directory_not_supported_yet():
+def test_missing_checkpoint_directory_is_an_error():
     with pytest.raises(ov.GeneratorError) as e:
         ov.Generator.load(ov.released_config(), "/nonexistent")
     assert str(e.value).startswith("OmniVoice generator: ")

@@ -611,11 +611,14 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   if (epilogue == Epilogue::kPartial) {
     // Split slices are summed by the row kernel that reads the output
     // anyway: split until the grid covers most CUs, keeping >= 8 K steps
-    // per split for the DMA ring to overlap.
+    // per split for the DMA ring to overlap, or >= 4 while the grid stays
+    // within half the CUs (small M, where more work-groups pulling operands
+    // win over a full ring).
     for (const int s : {2, 3, 4, 6, 8}) {
       if (plan.tiles * splits >= 160)
         break;
-      if (k_steps % s == 0 && k_steps / s >= 8)
+      const int min_steps = plan.tiles * s <= 128 ? 4 : 8;
+      if (k_steps % s == 0 && k_steps / s >= min_steps)
         splits = s;
     }
     plan.splits = splits;

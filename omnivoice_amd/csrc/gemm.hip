@@ -189,17 +189,15 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p,
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       w[c] = weight[32 * c + j];
-    // Issue every position and rotary load before the arithmetic.
-    int position[8 * FM];
-#pragma unroll
-    for (int e = 0; e < 8 * FM; ++e)
-      position[e] = p.positions[min(row0 + RowOf(e, lane), p.m - 1)];
+    // Every rotary load is issued before the arithmetic (one memory round
+    // trip: the table is already gathered per packed row).
     float2 cs[8 * FM][2];
 #pragma unroll
     for (int e = 0; e < 8 * FM; ++e)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        cs[e][c] = p.rope[static_cast<size_t>(position[e]) * 64 + 32 * c + j];
+        cs[e][c] = p.rope[static_cast<size_t>(min(row0 + RowOf(e, lane), p.m - 1)) * 64 +
+                          32 * c + j];
 #pragma unroll
     for (int e = 0; e < 8 * FM; ++e) {
       const int m = row0 + RowOf(e, lane);

@@ -90,8 +90,8 @@ struct GemmParams {
   int ldvt;
   const float* q_norm;
   const float* k_norm;
-  const float2* rope;      // [position][head_dim / 2] (cos, sin)
-  const int* positions;    // [M]
+  const float2* rope;      // [M][head_dim / 2]: (cos, sin) of each row's
+                           // position (LaunchRopeRows)
   int heads, kv_heads;
   float eps;
   // kSwiGlu
@@ -157,6 +157,11 @@ void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
                       int rows, int heads, int kv_heads, hipStream_t stream);
 
 void LaunchFill(int* data, int value, int count, hipStream_t stream);
+
+// rows_table[r][i] = table[positions[r]][i], i < 64, r < rows: the rotary
+// (cos, sin) pairs of every packed row, gathered once per batch layout.
+void LaunchRopeRows(const float2* table, const int* positions, int rows,
+                    float2* rows_table, hipStream_t stream);
 
 // ---------------------------------------------------------------- attention
 struct AttentionWork {

@@ -207,6 +207,13 @@ __global__ void TransposeVKernel(const half_t* qkv, int ld_qkv, half_t* vt,
       qkv[static_cast<size_t>(row) * ld_qkv + (heads + kv_heads + g) * 128 + d];
 }
 
+__global__ void RopeRowsKernel(const float2* table, const int* positions,
+                               int rows, float2* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < rows * 64)
+    out[i] = table[static_cast<size_t>(positions[i / 64]) * 64 + i % 64];
+}
+
 __global__ void FillKernel(int* data, int value, int count) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < count)
@@ -263,6 +270,14 @@ void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
   Dispatch(TransposeVKernel, grid, dim3(256), 0, stream, true, true, qkv,
            ld_qkv, vt, ldvt, rows, heads, kv_heads);
   Check(hipGetLastError(), "transpose launch");
+}
+
+void LaunchRopeRows(const float2* table, const int* positions, int rows,
+                    float2* rows_table, hipStream_t stream) {
+  Require(rows > 0, "rotary rows: no rows");
+  Dispatch(RopeRowsKernel, dim3((rows * 64 + 255) / 256), dim3(256), 0, stream,
+           true, true, table, positions, rows, rows_table);
+  Check(hipGetLastError(), "rotary rows launch");
 }
 
 void LaunchFill(int* data, int value, int count, hipStream_t stream) {

@@ -264,7 +264,8 @@ class Engine {
 
   DeviceBuffer<float> text_, audio_, final_norm_;
   DeviceBuffer<half_t> heads_;  // rows padded to a multiple of 128
-  DeviceBuffer<float2> rope_;
+  DeviceBuffer<float2> rope_;       // [max_positions][64]
+  DeviceBuffer<float2> rope_rows_;  // [rows_alloc][64], per packed row
   std::vector<Layer> layers_;
 
   // Workspace of the packed batch.
@@ -498,7 +499,7 @@ void Engine::LoadHost(const ovg_host_weights& w) {
 
 std::int64_t Engine::DeviceBytes() const {
   std::size_t total = text_.bytes() + audio_.bytes() + final_norm_.bytes() +
-                      heads_.bytes() + rope_.bytes();
+                      heads_.bytes() + rope_.bytes() + rope_rows_.bytes();
   for (const Layer& L : layers_)
     total += L.qkv.bytes() + L.output.bytes() + L.gate_up.bytes() +
              L.down.bytes() + L.input_norm.bytes() + L.post_norm.bytes() +
@@ -630,6 +631,7 @@ void Engine::Prepare(const Layout& L) {
   Grow(ids_, C * ra);
   Grow(row_kind_, ra);
   Grow(positions_, ra);
+  Grow(rope_rows_, ra * 64);
   Grow(gather_, static_cast<std::size_t>(L.targets));
   Grow(epoch_, 1);
   Grow(work_, L.work.size());
@@ -669,6 +671,8 @@ void Engine::Prepare(const Layout& L) {
   up(ids_.get(), L.ids.data(), L.ids.size() * sizeof(int));
   up(row_kind_.get(), L.row_kind.data(), L.row_kind.size() * sizeof(int));
   up(positions_.get(), L.positions.data(), L.positions.size() * sizeof(int));
+  LaunchRopeRows(rope_.get(), positions_.get(), L.rows_alloc, rope_rows_.get(),
+                 stream_);
   up(gather_.get(), L.gather.data(), L.gather.size() * sizeof(int));
   up(work_.get(), L.work.data(), L.work.size() * sizeof(AttentionWork));
   up(score_items_.get(), L.score_items.data(),
@@ -783,8 +787,7 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
            p.ldvt = ldvt;
            p.q_norm = W.q_norm.get();
            p.k_norm = W.k_norm.get();
-           p.rope = rope_.get();
-           p.positions = positions_.get();
+           p.rope = rope_rows_.get();
            p.heads = static_cast<int>(cfg_.heads);
            p.kv_heads = static_cast<int>(cfg_.kv_heads);
            p.eps = cfg_.rms_norm_eps;

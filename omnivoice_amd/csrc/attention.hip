@@ -5,13 +5,16 @@
 // 161-189). Scores never leave registers.
 //
 // A work-group takes one tile of 32 queries of one sequence and one key/value
-// head g, with 4 x GROUP compute waves (the GROUP query heads of g times four
-// key quarters) and one producer wave. Keys come in 32-key tiles (K [32][128]
-// and V^T [128][32], 16 KB), fetched global -> LDS by DMA into an 8-slot
-// ring, four tiles (a round) at a time; the producer fetches round r + 1
-// while the compute waves work on round r, quarter q taking tile 4 r + q.
-// Each tile is read from memory once for the whole head group (no GQA
-// repeat), and the group's query tiles come into LDS the same way, once. At
+// head g, with 4 x GROUP waves (the GROUP query heads of g times four key
+// quarters). Keys come in 32-key tiles (K [32][128] and V^T [128][32],
+// 16 KB), fetched global -> LDS by DMA into an 8-slot ring, four tiles (a
+// round) at a time, quarter q taking tile 4 r + q of round r. Every wave
+// issues an equal share of each round's 64 one-KB DMAs (a single issuing
+// wave would stall once 63 loads are in flight, the most its wait counter
+// tracks); rounds 0 and 1 go out at once, round r + 2 as soon as barrier
+// r + 1 frees round r's half of the ring. Each tile is read from memory once
+// for the whole head group (no GQA repeat), and the group's query tiles come
+// into LDS the same way, once. At
 // the end every wave leaves its online-softmax state in LDS and wave
 // (head, quarter q) merges the four quarters' states for dims 32 q .. 32 q +
 // 31 of its head in a fixed order, ((0 + 1) + (2 + 3)), and stores them.
@@ -107,9 +110,12 @@ __device__ __forceinline__ Slice Merge(const Slice& a, const Slice& b) {
 }
 
 template <int GROUP>
-__global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
+__global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
     AttentionParams p) {
-  constexpr int kWaves = 4 * GROUP;  // compute waves; wave kWaves feeds them
+  constexpr int kWaves = 4 * GROUP;
+  constexpr int kShare = 64 / kWaves;       // DMAs per wave and round
+  constexpr int kQShare = 8 * GROUP / kWaves;  // query DMAs per wave
+  static_assert(kShare % 8 == 0, "a share covers whole 8 KB halves of a tile");
   extern __shared__ __align__(16) unsigned char lds[];
   // Work-groups go round-robin over the 8 XCDs: block b takes kv head
   // b % kv_heads, so with 8 kv heads each XCD's L2 holds one head's keys,
@@ -129,8 +135,8 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 
   // DMA plan: instruction i of a round (64 of them) loads 1 KB of tile
   // 4 r + i / 16; part (i / 8) % 2 is K or V^T, sub = i % 8 its 1 KB block.
-  // One producer wave issues them all, so that no compute wave ever stalls
-  // on a full memory queue; tiles past the sequence reload its last tile.
+  // Wave w issues instructions kShare w .. kShare (w + 1) - 1; tiles past
+  // the sequence reload its last tile.
   const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
       p.qk + (p.heads + g) * kHeadDim);
   const unsigned char* v_base = reinterpret_cast<const unsigned char*>(
@@ -158,10 +164,11 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
   auto issue = [&](int r) {
     const int round = round_of(r);
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
+    for (int j = 0; j < kShare; ++j) {
+      const int i = wave * kShare + j;
       const int slot_in_round = i / 16;
       const int part = (i / 8) & 1;
-      const int sub = i & 7;
+      const int sub = j & 7;  // = i & 7
       const int t = min(round * kRound + slot_in_round, tiles - 1);
       const int key0 = work.seq_begin + t * kKTile;
       const uint32_t dst = lds_base + ((r & 1) * kRound + slot_in_round) * kTileBytes +
@@ -176,35 +183,27 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     }
   };
 
-  if (wave == kWaves) {
-    // The producer: the group's query tiles (laid out like a K tile; query
-    // rows past the tile's count repeat its last row, whose results are
-    // never stored) and round 0, then round r + 1 while round r is computed.
-    // Its barriers pair one to one with the compute waves'.
+  // The group's query tiles (laid out like a K tile; query rows past the
+  // tile's count repeat its last row, whose results are never stored), then
+  // rounds 0 and 1.
 #pragma unroll
-    for (int i = 0; i < 8 * GROUP; ++i) {
-      const int h = i >> 3, sub = i & 7;
-      const int row = min(4 * sub + (lane >> 4), work.q_count - 1);
-      const int chunk = (lane & 15) ^ ((4 * sub + (lane >> 4)) & 15);
-      DmaToLds(reinterpret_cast<const unsigned char*>(
-                   p.qk + static_cast<size_t>(work.q_begin) * p.ld_qk +
-                   (g * GROUP + h) * kHeadDim),
-               static_cast<uint32_t>(row * p.ld_qk + 8 * chunk) * 2,
-               lds_base + kRingBytes + h * kQBytes + sub * 1024);
-    }
-    issue(0);
+  for (int j = 0; j < kQShare; ++j) {
+    const int i = wave * kQShare + j;
+    const int h = i >> 3, sub = i & 7;
+    const int row = min(4 * sub + (lane >> 4), work.q_count - 1);
+    const int chunk = (lane & 15) ^ ((4 * sub + (lane >> 4)) & 15);
+    DmaToLds(reinterpret_cast<const unsigned char*>(
+                 p.qk + static_cast<size_t>(work.q_begin) * p.ld_qk +
+                 (g * GROUP + h) * kHeadDim),
+             static_cast<uint32_t>(row * p.ld_qk + 8 * chunk) * 2,
+             lds_base + kRingBytes + h * kQBytes + sub * 1024);
+  }
+  issue(0);
+  if (rounds > 1) {
+    issue(1);
+    WaitLoads<kShare>();  // this wave's queries and round 0 landed
+  } else {
     WaitLoads<0>();
-    RingBarrier();
-    for (int r = 0; r < rounds; ++r) {
-      if (r + 1 < rounds) {
-        issue(r + 1);
-        WaitLoads<0>();
-      }
-      RingBarrier();
-    }
-    __syncthreads();
-    __syncthreads();
-    return;
   }
   State st;
   st.max = -__builtin_inff();
@@ -227,9 +226,9 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
       v_read[dt][j2] = 8192 + d * 64 + (((2 * j2 + half_id) ^ ((d >> 2) & 3)) * 16);
   }
 
-  // Barrier r: round r has landed (the producer waited for it) and every
-  // compute wave is done with round r - 1, whose ring half the producer
-  // refills with round r + 1 meanwhile.
+  // Barrier r: round r has landed (every wave waited for its share) and
+  // every wave is done with round r - 1, whose ring half then takes round
+  // r + 1.
   RingBarrier();
   // Q^T operand: lane supplies dims 16 kk + 8 half_id .. +7 of query col.
   half8 qf[8];
@@ -285,7 +284,11 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
                             pb, st.o[dt]);
       }
     }
-    RingBarrier();  // barrier r + 1
+    if (r + 1 < rounds)
+      WaitLoads<0>();  // this wave's share of round r + 1 (the only round in flight)
+    RingBarrier();     // barrier r + 1
+    if (r + 2 < rounds)
+      issue(r + 2);
   }
 
   // Every wave leaves (max, sum) as a float2 and O^T as 16 float4 per lane;
@@ -351,11 +354,11 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   const dim3 grid(p.work_count * p.kv_heads);
   switch (group) {
     case 1:
-      Dispatch(AttentionKernel<1>, grid, dim3(5 * 64), AttentionLds<1>(), stream,
+      Dispatch(AttentionKernel<1>, grid, dim3(4 * 64), AttentionLds<1>(), stream,
                true, true, p);
       break;
     case 2:
-      Dispatch(AttentionKernel<2>, grid, dim3(9 * 64), AttentionLds<2>(), stream,
+      Dispatch(AttentionKernel<2>, grid, dim3(8 * 64), AttentionLds<2>(), stream,
                true, true, p);
       break;
     default:

@@ -8,10 +8,12 @@
 // head g, with 4 x GROUP waves (the GROUP query heads of g times four key
 // quarters). Keys come in 32-key tiles (K [32][128] and V^T [128][32],
 // 16 KB), fetched global -> LDS by DMA into an 8-slot ring, four tiles (a
-// round) at a time, quarter q taking tile 4 r + q of round r. Every wave
-// issues an equal share of each round's 64 one-KB DMAs (a single issuing
-// wave would stall once 63 loads are in flight, the most its wait counter
-// tracks); rounds 0 and 1 go out at once, round r + 2 as soon as barrier
+// round) at a time, quarter q taking tile 4 r + q of round r. The queries
+// and rounds 0 and 1 (both ring halves are free at the start) are fetched
+// by all compute waves, an equal share each: the 144 one-KB DMAs would
+// stall a single wave, whose wait counter tracks at most 63 loads. Later
+// rounds come from one extra producer wave, so that no compute wave blocks
+// on a full memory queue between rounds: round r + 2 as soon as barrier
 // r + 1 frees round r's half of the ring. Each tile is read from memory once
 // for the whole head group (no GQA repeat), and the group's query tiles come
 // into LDS the same way, once. At
@@ -31,6 +33,8 @@
 //
 // LDS rows are XOR-swizzled in 16-byte chunks (K: chunk ^ (key & 15); V^T:
 // chunk ^ ((dim >> 2) & 3)) so that both operand reads are conflict-free.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace ovg {
@@ -110,9 +114,9 @@ __device__ __forceinline__ Slice Merge(const Slice& a, const Slice& b) {
 }
 
 template <int GROUP>
-__global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
+__global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     AttentionParams p) {
-  constexpr int kWaves = 4 * GROUP;
+  constexpr int kWaves = 4 * GROUP;  // compute waves; wave kWaves: producer
   constexpr int kShare = 64 / kWaves;       // DMAs per wave and round
   constexpr int kQShare = 8 * GROUP / kWaves;  // query DMAs per wave
   static_assert(kShare % 8 == 0, "a share covers whole 8 KB halves of a tile");
@@ -135,7 +139,8 @@ __global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
 
   // DMA plan: instruction i of a round (64 of them) loads 1 KB of tile
   // 4 r + i / 16; part (i / 8) % 2 is K or V^T, sub = i % 8 its 1 KB block.
-  // Wave w issues instructions kShare w .. kShare (w + 1) - 1; tiles past
+  // Rounds 0 and 1: compute wave w issues instructions kShare w ..
+  // kShare (w + 1) - 1; later rounds: the producer issues all 64. Tiles past
   // the sequence reload its last tile.
   const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
       p.qk + (p.heads + g) * kHeadDim);
@@ -161,14 +166,14 @@ __global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
     const int k = r + shift;
     return k >= rounds ? k - rounds : k;
   };
-  auto issue = [&](int r) {
+  auto issue = [&](int r, int first, auto count) {
     const int round = round_of(r);
 #pragma unroll
-    for (int j = 0; j < kShare; ++j) {
-      const int i = wave * kShare + j;
+    for (int j = 0; j < decltype(count)::value; ++j) {
+      const int i = first + j;
       const int slot_in_round = i / 16;
       const int part = (i / 8) & 1;
-      const int sub = j & 7;  // = i & 7
+      const int sub = j & 7;  // = i & 7: first is a multiple of 8
       const int t = min(round * kRound + slot_in_round, tiles - 1);
       const int key0 = work.seq_begin + t * kKTile;
       const uint32_t dst = lds_base + ((r & 1) * kRound + slot_in_round) * kTileBytes +
@@ -183,6 +188,24 @@ __global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
     }
   };
 
+  using Share = std::integral_constant<int, kShare>;
+  using Round = std::integral_constant<int, 64>;
+  if (wave == kWaves) {
+    // The producer: round r + 2 once barrier r + 1 has freed its ring half,
+    // and waits for it before barrier r + 2. Its barriers pair one to one
+    // with the compute waves'.
+    RingBarrier();
+    for (int r = 0; r < rounds; ++r) {
+      if (r + 1 >= 2 && r + 1 < rounds)
+        WaitLoads<0>();
+      RingBarrier();
+      if (r + 2 < rounds)
+        issue(r + 2, 0, Round{});
+    }
+    __syncthreads();
+    __syncthreads();
+    return;
+  }
   // The group's query tiles (laid out like a K tile; query rows past the
   // tile's count repeat its last row, whose results are never stored), then
   // rounds 0 and 1.
@@ -198,9 +221,9 @@ __global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
              static_cast<uint32_t>(row * p.ld_qk + 8 * chunk) * 2,
              lds_base + kRingBytes + h * kQBytes + sub * 1024);
   }
-  issue(0);
+  issue(0, wave * kShare, Share{});
   if (rounds > 1) {
-    issue(1);
+    issue(1, wave * kShare, Share{});
     WaitLoads<kShare>();  // this wave's queries and round 0 landed
   } else {
     WaitLoads<0>();
@@ -284,11 +307,9 @@ __global__ __launch_bounds__(4 * GROUP * 64) void AttentionKernel(
                             pb, st.o[dt]);
       }
     }
-    if (r + 1 < rounds)
-      WaitLoads<0>();  // this wave's share of round r + 1 (the only round in flight)
+    if (r == 0 && rounds > 1)
+      WaitLoads<0>();  // this wave's share of round 1
     RingBarrier();     // barrier r + 1
-    if (r + 2 < rounds)
-      issue(r + 2);
   }
 
   // Every wave leaves (max, sum) as a float2 and O^T as 16 float4 per lane;
@@ -354,11 +375,11 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   const dim3 grid(p.work_count * p.kv_heads);
   switch (group) {
     case 1:
-      Dispatch(AttentionKernel<1>, grid, dim3(4 * 64), AttentionLds<1>(), stream,
+      Dispatch(AttentionKernel<1>, grid, dim3(5 * 64), AttentionLds<1>(), stream,
                true, true, p);
       break;
     case 2:
-      Dispatch(AttentionKernel<2>, grid, dim3(8 * 64), AttentionLds<2>(), stream,
+      Dispatch(AttentionKernel<2>, grid, dim3(9 * 64), AttentionLds<2>(), stream,
                true, true, p);
       break;
     default:

@@ -536,15 +536,17 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
 
 // Sums a tile's split-K partials in split order 0, 1, ... (a fixed order,
 // reproducible bit for bit) in the same per-wave layout the GEMM kernel
-// stored them in, and applies the epilogue.
+// stored them in, and applies the epilogue. One single-wave work-group per
+// (tile, GEMM wave): each wave's epilogue stands alone, and spreading the
+// partials over that many CUs keeps every CU's share of the reads small.
 template <Epilogue EPI, int FM>
-__global__ __launch_bounds__(Shape<FM>::kThreads) void SplitReduceKernel(
-    GemmParams p, int tiles_m) {
+__global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
+                                                       int tiles_m) {
   using S = Shape<FM>;
   constexpr int kQuads = 2 * FM;
-  const int tile = blockIdx.x;
+  const int tile = blockIdx.x / S::kWaves;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = blockIdx.x % S::kWaves;
   const size_t split_stride = static_cast<size_t>(S::kWaves) * 4 * kQuads * 64;
   const floatx4* base = reinterpret_cast<const floatx4*>(p.partials) +
                         static_cast<size_t>(tile) * p.splits * split_stride +
@@ -571,8 +573,8 @@ void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
   Dispatch(GemmKernel<STAGES, EPI, FM>, dim3(groups), dim3(Shape<FM>::kThreads),
            LdsBytes<STAGES, FM>(), stream, true, !reduce, p, tiles_m);
   if (reduce)
-    Dispatch(SplitReduceKernel<EPI, FM>, dim3(groups / p.splits),
-             dim3(Shape<FM>::kThreads), 0, stream, false, true, p, tiles_m);
+    Dispatch(SplitReduceKernel<EPI, FM>, dim3(groups / p.splits * Shape<FM>::kWaves),
+             dim3(64), 0, stream, false, true, p, tiles_m);
 }
 
 template <Epilogue EPI, int FM>

@@ -133,13 +133,15 @@ __global__ __launch_bounds__(kRowThreads) void RmsNormKernel(
   }
 }
 
-// Residual update + RMSNorm (see AddNormParams), one wave per row. All of a
-// row's loads (hidden and every split slice) are issued before the sum, which
-// then runs in the fixed order hidden + slice 0 + slice 1 + ...
+// Residual update + RMSNorm (see AddNormParams), one single-wave work-group
+// per row, so that the row's reads (up to 9 rows of 4 KB) spread over as
+// many CUs as there are rows. All of a row's loads (hidden and every split
+// slice) are issued before the sum, which then runs in the fixed order
+// hidden + slice 0 + slice 1 + ...
 template <int CHUNKS, int MAX_SPLITS>
-__global__ __launch_bounds__(kRowThreads) void AddNormKernel(AddNormParams p) {
+__global__ __launch_bounds__(64) void AddNormKernel(AddNormParams p) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  const int r = blockIdx.x;
   if (r >= p.rows)
     return;
   const int src = p.gather != nullptr ? p.gather[r] : r;
@@ -253,13 +255,11 @@ void LaunchAddNorm(const AddNormParams& p, hipStream_t stream) {
   Require(p.width % 4 == 0 && p.width <= 1024,
           "addnorm: width must be a multiple of 4 and at most 1024");
   Require(p.splits >= 1 && p.splits <= 8, "addnorm: 1 to 8 partial slices");
-  const dim3 grid((p.rows + kRowThreads / 64 - 1) / (kRowThreads / 64));
+  const dim3 grid(p.rows);
   if (p.splits <= 4)
-    Dispatch(AddNormKernel<4, 4>, grid, dim3(kRowThreads), 0, stream, true,
-             true, p);
+    Dispatch(AddNormKernel<4, 4>, grid, dim3(64), 0, stream, true, true, p);
   else
-    Dispatch(AddNormKernel<4, 8>, grid, dim3(kRowThreads), 0, stream, true,
-             true, p);
+    Dispatch(AddNormKernel<4, 8>, grid, dim3(64), 0, stream, true, true, p);
   Check(hipGetLastError(), "addnorm launch");
 }
 

@@ -312,27 +312,39 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     RingBarrier();     // barrier r + 1
   }
 
-  // Every wave leaves (max, sum) as a float2 and O^T as 16 float4 per lane;
-  // wave (head, quarter) then merges dims 32 quarter .. +31 of its head.
+  // Every wave leaves (max, sum) as a float2 and the three dim slices of
+  // O^T that other waves merge (4 float4 per lane each); wave (head,
+  // quarter) then merges dims 32 quarter .. +31 of its head, its own
+  // quarter's part straight from registers.
   float2* pairs = reinterpret_cast<float2*>(lds);
   floatx4* accs = reinterpret_cast<floatx4*>(lds + kWaves * 64 * 8);
   __syncthreads();
   pairs[wave * 64 + lane] = float2{st.max, st.sum};
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < 4; ++dt) {
+    if (dt == quarter)
+      continue;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       accs[(wave * 16 + dt * 4 + k) * 64 + lane] =
           floatx4{st.o[dt][4 * k], st.o[dt][4 * k + 1], st.o[dt][4 * k + 2],
                   st.o[dt][4 * k + 3]};
+  }
   __syncthreads();
   const int dt = quarter;
+  // This wave's own slice, selected without indexing the register array by
+  // a runtime value.
+  const floatx16 own = dt == 0 ? st.o[0] : dt == 1 ? st.o[1] : dt == 2 ? st.o[2] : st.o[3];
   auto load = [&](int q) {
     const int w = q * GROUP + head_local;
     const float2 ms = pairs[w * 64 + lane];
     Slice sl;
     sl.max = ms.x;
     sl.sum = ms.y;
+    if (q == quarter) {
+      sl.o = own;
+      return sl;
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const floatx4 v = accs[(w * 16 + dt * 4 + k) * 64 + lane];

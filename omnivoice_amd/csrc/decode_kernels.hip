@@ -29,15 +29,14 @@ constexpr float kLog2e = 1.44269504088896341F;
 constexpr float kLn2Head = 0.693359375F;
 constexpr float kLn2Tail = -2.12194440054690583e-4F;
 
+// Branch-free: the polynomial runs on x clamped to [-87, 88] (which leaves
+// every in-range x untouched), then selects give 0 below the range, +inf
+// above it and NaN for NaN, the values of the early returns of the CPU
+// restatement.
 __device__ __forceinline__ float ExpExact(float x) {
-  if (x != x)
-    return x;
-  if (x < -87.0F)
-    return 0.0F;
-  if (x > 88.0F)
-    return __builtin_inff();
-  const float n = __builtin_rintf(x * kLog2e);
-  float r = __builtin_fmaf(n, -kLn2Head, x);
+  const float xc = fminf(fmaxf(x, -87.0F), 88.0F);
+  const float n = __builtin_rintf(xc * kLog2e);
+  float r = __builtin_fmaf(n, -kLn2Head, xc);
   r = __builtin_fmaf(n, -kLn2Tail, r);
   float p = 1.0F / 5040.0F;
   p = __builtin_fmaf(p, r, 1.0F / 720.0F);
@@ -49,7 +48,10 @@ __device__ __forceinline__ float ExpExact(float x) {
   p = __builtin_fmaf(p, r, 1.0F);
   const int e = static_cast<int>(n);
   const float scale = __uint_as_float(static_cast<unsigned>(e + 127) << 23);
-  return p * scale;
+  float y = p * scale;
+  y = x < -87.0F ? 0.0F : y;
+  y = x > 88.0F ? __builtin_inff() : y;
+  return x != x ? x : y;
 }
 
 __device__ __forceinline__ float LogExact(float x) {
@@ -104,27 +106,26 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void ScoreKernel(
                     static_cast<size_t>(item.logit_row + frame) * p.width +
                     codebook * p.vocab;
   const float* ur = cr + static_cast<size_t>(item.frames) * p.width;
+  // Entries past the vocabulary hold -inf: they leave every max unchanged
+  // and add exp(-inf) = +0 to every per-lane sum, which is exactly the sum
+  // without them, so the arithmetic needs no per-entry branches.
   float cv[kScorePerLane], uv[kScorePerLane];
   float cm = -3.402823466e38F, um = -3.402823466e38F;
 #pragma unroll
   for (int t = 0; t < kScorePerLane; ++t) {
     const int j = lane + t * kWave;
-    if (j < p.vocab) {
-      cv[t] = cr[j];
-      uv[t] = ur[j];
-      cm = fmaxf(cm, cv[t]);
-      um = fmaxf(um, uv[t]);
-    }
+    cv[t] = j < p.vocab ? cr[j] : -__builtin_inff();
+    uv[t] = j < p.vocab ? ur[j] : -__builtin_inff();
+    cm = fmaxf(cm, cv[t]);
+    um = fmaxf(um, uv[t]);
   }
   cm = WaveMax(cm);
   um = WaveMax(um);
   float cs = 0.0F, us = 0.0F;
 #pragma unroll
   for (int t = 0; t < kScorePerLane; ++t) {
-    if (lane + t * kWave < p.vocab) {
-      cs = cs + ExpExact(cv[t] - cm);
-      us = us + ExpExact(uv[t] - um);
-    }
+    cs = cs + ExpExact(cv[t] - cm);
+    us = us + ExpExact(uv[t] - um);
   }
   const float c_lse = cm + LogExact(WaveSum(cs));
   const float u_lse = um + LogExact(WaveSum(us));
@@ -132,12 +133,11 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void ScoreKernel(
   float gm = -3.402823466e38F;
 #pragma unroll
   for (int t = 0; t < kScorePerLane; ++t) {
-    if (lane + t * kWave < p.vocab) {
-      const float c = cv[t] - c_lse;
-      const float u = uv[t] - u_lse;
-      gv[t] = __builtin_fmaf(p.guidance, c - u, c);
-      gm = fmaxf(gm, gv[t]);
-    }
+    const float c = cv[t] - c_lse;
+    const float u = uv[t] - u_lse;
+    gv[t] = lane + t * kWave < p.vocab ? __builtin_fmaf(p.guidance, c - u, c)
+                                       : -__builtin_inff();
+    gm = fmaxf(gm, gv[t]);
   }
   gm = WaveMax(gm);
   float gs = 0.0F;
@@ -146,13 +146,11 @@ __global__ __launch_bounds__(kScoreWaves * kWave) void ScoreKernel(
 #pragma unroll
   for (int t = 0; t < kScorePerLane; ++t) {
     const int j = lane + t * kWave;
-    if (j < p.vocab) {
-      gs = gs + ExpExact(gv[t] - gm);
-      if (j != static_cast<int>(p.mask_id) && gv[t] > best) {
-        best = gv[t];
-        best_index = j;
-      }
-    }
+    gs = gs + ExpExact(gv[t] - gm);
+    // -inf (past the vocabulary) never beats the initial best.
+    const bool better = j != static_cast<int>(p.mask_id) && gv[t] > best;
+    best = better ? gv[t] : best;
+    best_index = better ? j : best_index;
   }
   const float g_lse = gm + LogExact(WaveSum(gs));
   for (int offset = kWave / 2; offset > 0; offset /= 2) {

@@ -190,9 +190,15 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
     return;
   const int total = p.codebooks * item.frames;
   const int tid = threadIdx.x;
+  // Key slots in use (the same for every thread): each loop below is
+  // unrolled, so the keys stay in registers, and leaves after `slots`
+  // iterations, so a 2000-key item costs 2 slots' work, not 16.
+  const int slots = (total + kSelectThreads - 1) / kSelectThreads;
   uint64_t key[kSelectPerThread];
 #pragma unroll
   for (int r = 0; r < kSelectPerThread; ++r) {
+    if (r >= slots)
+      break;
     const int i = tid + r * kSelectThreads;
     key[r] = 0;
     if (i < total) {
@@ -219,6 +225,8 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
     const uint64_t high = prefix >> (shift + 8);
 #pragma unroll
     for (int r = 0; r < kSelectPerThread; ++r) {
+      if (r >= slots)
+        break;
       const int i = tid + r * kSelectThreads;
       if (i < total && (key[r] >> (shift + 8)) == high)
         atomicAdd(&histogram[(key[r] >> shift) & 0xFF], 1U);
@@ -254,6 +262,8 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
   // prefix is now the count-th largest key: everything >= it is chosen.
 #pragma unroll
   for (int r = 0; r < kSelectPerThread; ++r) {
+    if (r >= slots)
+      break;
     const int i = tid + r * kSelectThreads;
     if (i < total && key[r] >= prefix) {
       const int value = p.prediction[item.out_base + i];

@@ -90,6 +90,55 @@ __global__ __launch_bounds__(kRowThreads) void EmbedKernel(EmbedParams p) {
   }
 }
 
+// The same for the released shape (8 codebooks, hidden 1024: one float4 per
+// thread), with no branch before the arithmetic: every id, then every
+// embedding row, is loaded unconditionally (unused codebooks of text and
+// padding rows re-read the row's first entry, a cache hit), and the sum
+// selects the rows in use. A row then costs two memory round trips instead
+// of one per conditionally loaded row. The sum runs in codebook order from
+// +0, as in EmbedKernel (adding +0 for an unused codebook leaves it
+// unchanged).
+__global__ __launch_bounds__(kRowThreads) void Embed8Kernel(EmbedParams p) {
+  constexpr int kCodebooks = 8;
+  __shared__ float scratch[4];
+  const int row = blockIdx.x;
+  if (p.epoch != nullptr && row == 0 && threadIdx.x == 0)
+    *p.epoch += 1;
+  const int kind = p.row_kind[row];
+  const int count = kind == 1 ? kCodebooks : (kind == 0 ? 1 : 0);
+  int id[kCodebooks];
+#pragma unroll
+  for (int c = 0; c < kCodebooks; ++c)
+    id[c] = p.ids[static_cast<size_t>(c) * p.ld_ids + row];
+  const float* table = kind == 0 ? p.text : p.audio;
+  const int d = threadIdx.x * 4;
+  const floatx4 w = *reinterpret_cast<const floatx4*>(p.norm + d);
+  floatx4 e[kCodebooks];
+#pragma unroll
+  for (int c = 0; c < kCodebooks; ++c) {
+    const int entry = kind == 0 ? id[0] : c * p.vocab + id[c];
+    e[c] = *reinterpret_cast<const floatx4*>(
+        table + static_cast<size_t>(entry) * p.hidden_size + d);
+  }
+  floatx4 v = {0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < kCodebooks; ++c)
+    v += c < count ? e[c] : floatx4{0, 0, 0, 0};
+  float* out = p.hidden + static_cast<size_t>(row) * p.hidden_size;
+  *reinterpret_cast<floatx4*>(out + d) = v;
+  const float squares =
+      v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  const float total = BlockSum(squares, scratch);
+  const float scale =
+      rsqrtf(total / static_cast<float>(p.hidden_size) + p.eps);
+  half_t* normed = p.normed + static_cast<size_t>(row) * p.hidden_size;
+  *reinterpret_cast<half4*>(normed + d) =
+      half4{static_cast<half_t>(w[0] * (v[0] * scale)),
+            static_cast<half_t>(w[1] * (v[1] * scale)),
+            static_cast<half_t>(w[2] * (v[2] * scale)),
+            static_cast<half_t>(w[3] * (v[3] * scale))};
+}
+
 // One wave per row, four rows per work-group: lane l owns the float4
 // columns 4 (l + 64 i), so every load is a contiguous 1 KB per wave and the
 // row sum of squares is one wave butterfly (no barriers). CHUNKS float4 per
@@ -229,8 +278,12 @@ void LaunchEmbed(const EmbedParams& p, hipStream_t stream) {
   Require(p.hidden_size % 4 == 0 && p.hidden_size <= 4 * 4 * kRowThreads,
           "embed: hidden size must be a multiple of 4 and at most 4096");
   Require(p.codebooks >= 1 && p.codebooks <= 16, "embed: 1 to 16 codebooks");
-  Dispatch(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream, true, true,
-           p);
+  if (p.codebooks == 8 && p.hidden_size == 4 * kRowThreads)
+    Dispatch(Embed8Kernel, dim3(p.rows), dim3(kRowThreads), 0, stream, true,
+             true, p);
+  else
+    Dispatch(EmbedKernel, dim3(p.rows), dim3(kRowThreads), 0, stream, true,
+             true, p);
   Check(hipGetLastError(), "embed launch");
 }
 

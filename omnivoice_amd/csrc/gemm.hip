@@ -551,16 +551,27 @@ __global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
   const floatx4* base = reinterpret_cast<const floatx4*>(p.partials) +
                         static_cast<size_t>(tile) * p.splits * split_stride +
                         wave * 4 * kQuads * 64 + lane;
+  // Split by split, each split's loads issued together (one memory round
+  // trip per split), summing in split order 0, 1, ...
+  floatx4 sum[4 * kQuads];
+#pragma unroll
+  for (int q = 0; q < 4 * kQuads; ++q)
+    sum[q] = base[q * 64];
+  for (int s = 1; s < p.splits; ++s) {
+    floatx4 next[4 * kQuads];
+#pragma unroll
+    for (int q = 0; q < 4 * kQuads; ++q)
+      next[q] = base[s * split_stride + q * 64];
+#pragma unroll
+    for (int q = 0; q < 4 * kQuads; ++q)
+      sum[q] += next[q];
+  }
   Owned<FM> own;
 #pragma unroll
-  for (int q = 0; q < 4 * kQuads; ++q) {
-    floatx4 sum = base[q * 64];
-    for (int s = 1; s < p.splits; ++s)
-      sum += base[s * split_stride + q * 64];
+  for (int q = 0; q < 4 * kQuads; ++q)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      own.v[q / kQuads][4 * (q % kQuads) + i] = sum[i];
-  }
+      own.v[q / kQuads][4 * (q % kQuads) + i] = sum[q][i];
   const int tile_m = tile % tiles_m;
   const int row0 = tile_m * kBM + 32 * FM * (wave % S::kStrips) +
                    16 * FM * (wave / S::kStrips);

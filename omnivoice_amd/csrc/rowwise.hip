@@ -246,6 +246,54 @@ __global__ __launch_bounds__(64) void AddNormKernel(AddNormParams p) {
   }
 }
 
+// The same for rows of 1024 (lane l owns float4 columns 4 (l + 64 i),
+// i < 4) with the slice count fixed at compile time: no load is
+// conditional, so all of a row's loads leave before the first returns (the
+// guarded loads of AddNormKernel let the compiler wait between them). The
+// arithmetic is AddNormKernel's, in the same order.
+template <int SPLITS>
+__global__ __launch_bounds__(64) void AddNorm1024Kernel(AddNormParams p) {
+  constexpr int kChunks = 4;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x;
+  const int src = p.gather != nullptr ? p.gather[r] : r;
+  float* h = p.hidden + static_cast<size_t>(src) * 1024;
+  const float* part = p.partials + static_cast<size_t>(src) * 1024;
+  floatx4 v[kChunks], wv[kChunks], parts[SPLITS][kChunks];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const int d = (lane + 64 * i) * 4;
+    v[i] = *reinterpret_cast<const floatx4*>(h + d);
+    wv[i] = *reinterpret_cast<const floatx4*>(p.norm + d);
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s)
+      parts[s][i] = *reinterpret_cast<const floatx4*>(part + s * p.split_stride + d);
+  }
+  float squares = 0.0F;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s)
+      v[i] += parts[s][i];
+    squares += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] +
+               v[i][3] * v[i][3];
+  }
+  if (p.gather == nullptr) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i)
+      *reinterpret_cast<floatx4*>(h + (lane + 64 * i) * 4) = v[i];
+  }
+  const float scale = rsqrtf(WaveSumFast(squares) / 1024.0F + p.eps);
+  half_t* o = p.out + static_cast<size_t>(r) * 1024;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i)
+    *reinterpret_cast<half4*>(o + (lane + 64 * i) * 4) =
+        half4{static_cast<half_t>(wv[i][0] * (v[i][0] * scale)),
+              static_cast<half_t>(wv[i][1] * (v[i][1] * scale)),
+              static_cast<half_t>(wv[i][2] * (v[i][2] * scale)),
+              static_cast<half_t>(wv[i][3] * (v[i][3] * scale))};
+}
+
 // One thread per (kv head, dim, row).
 __global__ void TransposeVKernel(const half_t* qkv, int ld_qkv, half_t* vt,
                                  int ldvt, int rows, int heads, int kv_heads) {
@@ -309,7 +357,18 @@ void LaunchAddNorm(const AddNormParams& p, hipStream_t stream) {
           "addnorm: width must be a multiple of 4 and at most 1024");
   Require(p.splits >= 1 && p.splits <= 8, "addnorm: 1 to 8 partial slices");
   const dim3 grid(p.rows);
-  if (p.splits <= 4)
+  if (p.width == 1024) {
+    switch (p.splits) {
+      case 1: Dispatch(AddNorm1024Kernel<1>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 2: Dispatch(AddNorm1024Kernel<2>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 3: Dispatch(AddNorm1024Kernel<3>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 4: Dispatch(AddNorm1024Kernel<4>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 5: Dispatch(AddNorm1024Kernel<5>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 6: Dispatch(AddNorm1024Kernel<6>, grid, dim3(64), 0, stream, true, true, p); break;
+      case 7: Dispatch(AddNorm1024Kernel<7>, grid, dim3(64), 0, stream, true, true, p); break;
+      default: Dispatch(AddNorm1024Kernel<8>, grid, dim3(64), 0, stream, true, true, p); break;
+    }
+  } else if (p.splits <= 4)
     Dispatch(AddNormKernel<4, 4>, grid, dim3(64), 0, stream, true, true, p);
   else
     Dispatch(AddNormKernel<4, 8>, grid, dim3(64), 0, stream, true, true, p);

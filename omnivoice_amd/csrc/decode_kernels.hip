@@ -177,26 +177,52 @@ __device__ __forceinline__ unsigned OrderedBits(float s) {
   return (u & 0x80000000U) ? ~u : (u | 0x80000000U);
 }
 
+// SLOTS: keys per thread the launch allows (4 covers items of up to 4096
+// positions in registers; 16 the API's maximum of 16384).
+template <int SLOTS>
 __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
     SelectParams p) {
   __shared__ unsigned histogram[256];
   __shared__ int chosen_digit;
   __shared__ int remaining;
   const SelectItem item = p.items[blockIdx.x];
-  SelectStep s = p.single;
-  if (p.epoch != nullptr)
-    s = p.plan[(*p.epoch - 1) * p.item_count + blockIdx.x];
-  if (s.count <= 0)
-    return;
   const int total = p.codebooks * item.frames;
   const int tid = threadIdx.x;
   // Key slots in use (the same for every thread): each loop below is
   // unrolled, so the keys stay in registers, and leaves after `slots`
   // iterations, so a 2000-key item costs 2 slots' work, not 16.
   const int slots = (total + kSelectThreads - 1) / kSelectThreads;
-  uint64_t key[kSelectPerThread];
+  // Every load that does not depend on the step (confidence, codes and
+  // predictions, unconditionally at clamped indices) is issued together
+  // with the step's plan entry, then the noise: three memory round trips in
+  // all instead of one per load.
+  float conf[SLOTS], noise[SLOTS];
+  int code[SLOTS], pred[SLOTS];
 #pragma unroll
-  for (int r = 0; r < kSelectPerThread; ++r) {
+  for (int r = 0; r < SLOTS; ++r) {
+    if (r >= slots)
+      break;
+    const int i = min(tid + r * kSelectThreads, total - 1);
+    conf[r] = p.confidence[item.out_base + i];
+    code[r] = p.codes[item.out_base + i];
+    pred[r] = p.prediction[item.out_base + i];
+  }
+  SelectStep s = p.single;
+  if (p.epoch != nullptr)
+    s = p.plan[(*p.epoch - 1) * p.item_count + blockIdx.x];
+  if (s.count <= 0)
+    return;
+  if (p.temperature > 0.0F) {
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+      if (r >= slots)
+        break;
+      noise[r] = p.noise[s.noise_offset + min(tid + r * kSelectThreads, total - 1)];
+    }
+  }
+  uint64_t key[SLOTS];
+#pragma unroll
+  for (int r = 0; r < SLOTS; ++r) {
     if (r >= slots)
       break;
     const int i = tid + r * kSelectThreads;
@@ -204,10 +230,10 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
     if (i < total) {
       const int c = i / item.frames;
       const float penalty = static_cast<float>(c) * p.layer_penalty;
-      float score = p.confidence[item.out_base + i] - penalty;
+      float score = conf[r] - penalty;
       if (p.temperature > 0.0F)
-        score = score / p.temperature + p.noise[s.noise_offset + i];
-      if (p.codes[item.out_base + i] != static_cast<int>(p.mask_id))
+        score = score / p.temperature + noise[r];
+      if (code[r] != static_cast<int>(p.mask_id))
         score = -__builtin_inff();
       key[r] = (static_cast<uint64_t>(OrderedBits(score)) << 16) |
                static_cast<uint64_t>(0xFFFF - i);
@@ -224,7 +250,7 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
     __syncthreads();
     const uint64_t high = prefix >> (shift + 8);
 #pragma unroll
-    for (int r = 0; r < kSelectPerThread; ++r) {
+    for (int r = 0; r < SLOTS; ++r) {
       if (r >= slots)
         break;
       const int i = tid + r * kSelectThreads;
@@ -261,12 +287,12 @@ __global__ __launch_bounds__(kSelectThreads) void SelectKernel(
   }
   // prefix is now the count-th largest key: everything >= it is chosen.
 #pragma unroll
-  for (int r = 0; r < kSelectPerThread; ++r) {
+  for (int r = 0; r < SLOTS; ++r) {
     if (r >= slots)
       break;
     const int i = tid + r * kSelectThreads;
     if (i < total && key[r] >= prefix) {
-      const int value = p.prediction[item.out_base + i];
+      const int value = pred[r];
       p.codes[item.out_base + i] = value;
       p.unmasked_at[item.out_base + i] = s.step;
       if (p.ids != nullptr) {
@@ -297,8 +323,12 @@ void LaunchSelect(const SelectParams& p, int max_total, hipStream_t stream) {
   Require(max_total >= 1 && max_total <= kSelectThreads * kSelectPerThread,
           "select: codebooks * frames outside [1, 16384]");
   Require(p.item_count >= 1, "select: no items");
-  Dispatch(SelectKernel, dim3(p.item_count), dim3(kSelectThreads), 0, stream,
-           true, true, p);
+  if (max_total <= 4 * kSelectThreads)
+    Dispatch(SelectKernel<4>, dim3(p.item_count), dim3(kSelectThreads), 0,
+             stream, true, true, p);
+  else
+    Dispatch(SelectKernel<kSelectPerThread>, dim3(p.item_count),
+             dim3(kSelectThreads), 0, stream, true, true, p);
   Check(hipGetLastError(), "select launch");
 }
 

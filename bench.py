@@ -13,6 +13,11 @@ final codes copied back. `value` is unmask steps per second
 (32 x utterances / wall time); `utterance_rtf` is wall time per utterance
 over 10 s.
 
+Other workloads (--workload): 2s, clone (5 s reference voice + 15 s target)
+and chunks (four 15 s chunks of long text generated as one batch through
+Generator::GenerateBatch; there `value` counts the unmask steps of all four
+items and `utterance_rtf` is wall time over the 60 s of audio).
+
 Also reported: the roofline of the dominant kernel (algorithmic FLOPs or
 bytes per launch over its HIP-event-timed launch duration on the library
 stream) and the CPU baseline (the oracle's float32 restatement of the
@@ -37,7 +42,10 @@ WORKLOADS = {
     "10s": (80, 0, 250),
     "2s": (20, 0, 50),
     "clone": (180, 125, 375),
+    # four chunks of long text, batched (4 CFG pairs packed as 8 rows)
+    "chunks": (110, 0, 375),
 }
+ITEMS = {"chunks": 4}  # items generated together (ovg_generate_batch)
 
 
 def make_input(ov, text, reference, target, seed=42):
@@ -110,7 +118,9 @@ def main():
 
     cfg = ov.released_config()
     text, reference, target = WORKLOADS[args.workload]
-    x = make_input(ov, text, reference, target)
+    items = ITEMS.get(args.workload, 1)
+    xs = [make_input(ov, text, reference, target, seed=42 + j) for j in range(items)]
+    x = xs[0]
     decoding = ov.DecodingConfig(steps=32, guidance=2.0, t_shift=0.1,
                                  layer_penalty=5.0, position_temperature=5.0)
     t0 = time.perf_counter()
@@ -118,19 +128,25 @@ def main():
     load_s = time.perf_counter() - t0
     executed = sum(1 for c in ov.unmask_schedule(8 * target, 32, 0.1) if c)
 
+    def run(i):
+        if items == 1:
+            gen.generate(x, decoding, seed=42 + i)
+        else:
+            gen.generate_batch(xs, decoding, seeds=[42 + i * items + j for j in range(items)])
+
     for i in range(args.warmup):
-        gen.generate(x, decoding, seed=42 + i)
+        run(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        gen.generate(x, decoding, seed=42 + i)
+        run(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_utterance = elapsed / args.steps * 1e3
-    steps_per_s = executed * args.steps / elapsed
-    rtf = (elapsed / args.steps) / (target / 25.0)
+    steps_per_s = executed * items * args.steps / elapsed
+    rtf = (elapsed / args.steps) / (items * target / 25.0)
 
-    stats = gen.profile(x, repeats=args.profile_repeats)
+    stats = gen.profile(xs if items > 1 else x, repeats=args.profile_repeats)
     kernels = {}
     for name, s in stats.items():
         avg = s["total_ms"] / s["launches"]
@@ -163,7 +179,7 @@ def main():
     if os.path.exists(traffic_path):
         with open(traffic_path) as f:
             measured = json.load(f).get(dominant)
-        if measured:
+        if measured and measured.get("workload") == args.workload:
             roofline["traffic"] = measured["bytes"]
             roofline["traffic_source"] = "profiles/" + measured["source"]
     gemm_ms = sum(s["total_ms"] for n, s in stats.items() if n.startswith("gemm_")
@@ -184,7 +200,13 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (seeded N(0, 0.02) fp16 weights, uniform text ids, masked target)",
-        "config": {"workload": f"{args.workload}: {text} text tokens, {reference} "
+        "config": {"workload": f"{args.workload}: {items} x ({text} text tokens, {reference} "
+                               f"reference frames, {target} masked target frames), "
+                               f"{items} CFG pair(s) packed as "
+                               f"{items * (text + reference + 2 * target)} rows, "
+                               f"32 steps, guidance 2.0, position temperature 5.0"
+                               if items > 1 else
+                               f"{args.workload}: {text} text tokens, {reference} "
                                f"reference frames, {target} masked target frames, "
                                f"CFG pair packed as {text + reference + 2 * target} rows, "
                                f"32 steps, guidance 2.0, position temperature 5.0",
@@ -198,7 +220,7 @@ def main():
         "kernels": kernels,
         "load_s": load_s,
     }
-    if args.cpu_steps > 0:
+    if args.cpu_steps > 0 and items == 1:
         result["cpu_baseline"] = cpu_baseline(cfg, x, decoding, args.cpu_steps)
     print(json.dumps(result), flush=True)
 

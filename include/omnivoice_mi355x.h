@@ -177,11 +177,20 @@ int ovg_generate_trace(ovg_handle* handle, const ovg_input* input,
                        size_t error_len);
 
 /* Per-kernel durations of one eager forward + score + select of `input`
- * (HIP events around every launch). Writes up to `capacity` entries. */
+ * (HIP events around every launch). Writes up to `capacity` entries and
+ * sets `count` to the number of distinct kernels. A measurement hook: the
+ * reference has no counterpart. */
 int ovg_profile_step(ovg_handle* handle, const ovg_input* input,
                      int64_t repeats, ovg_kernel_stat* stats,
                      int64_t capacity, int64_t* count, char* error,
                      size_t error_len);
+
+/* ovg_profile_step over `items` inputs packed as one batch, as
+ * ovg_generate_batch runs them. */
+int ovg_profile_batch(ovg_handle* handle, int64_t items,
+                      const ovg_input* inputs, int64_t repeats,
+                      ovg_kernel_stat* stats, int64_t capacity, int64_t* count,
+                      char* error, size_t error_len);
 
 /* Values the synthetic model holds for elements [first, first + count) of
  * one tensor (ids: text embeddings 1, audio embeddings 2, audio heads 3,

@@ -96,6 +96,8 @@ EXPORTS = {
                                           _ptr, ctypes.POINTER(_i64), _err, _sz]),
     "ovg_profile_step": (ctypes.c_int, [_ptr, ctypes.POINTER(_Input), _i64, _ptr, _i64,
                                         ctypes.POINTER(_i64), _err, _sz]),
+    "ovg_profile_batch": (ctypes.c_int, [_ptr, _i64, ctypes.POINTER(_Input), _i64, _ptr,
+                                         _i64, ctypes.POINTER(_i64), _err, _sz]),
     "ovg_device_bytes": (_i64, [_ptr]),
     "ovg_synthetic_values": (None, [_u64, _u64, _u64, _i64, ctypes.c_int, _f32, _ptr]),
     "ovg_unmask_schedule": (ctypes.c_int, [_i64, _i64, _f32, _ptr]),
@@ -394,16 +396,18 @@ class Generator:
                                         ctypes.byref(executed), err, len(err)), err)
         return GenerationResult(codes, at, executed.value, trace)
 
-    def profile(self, inp: ConditionalInput, repeats: int = 3) -> dict:
-        """Per-kernel HIP-event timings of eager forward + score + select."""
+    def profile(self, inp, repeats: int = 3) -> dict:
+        """Per-kernel HIP-event timings of eager forward + score + select of
+        one input, or of a list of inputs packed as one batch."""
+        items = list(inp) if isinstance(inp, (list, tuple)) else [inp]
         cap = 64
         stats = (_KernelStat * cap)()
         count = _i64()
-        c = inp._c()
+        cs = (_Input * len(items))(*[i._c() for i in items])
         err = _buf()
-        _check(lib().ovg_profile_step(self._h, ctypes.byref(c), repeats,
-                                      ctypes.cast(stats, _ptr), cap,
-                                      ctypes.byref(count), err, len(err)), err)
+        _check(lib().ovg_profile_batch(self._h, len(items), cs, repeats,
+                                       ctypes.cast(stats, _ptr), cap,
+                                       ctypes.byref(count), err, len(err)), err)
         out = {}
         for i in range(min(count.value, cap)):
             s = stats[i]

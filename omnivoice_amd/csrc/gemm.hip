@@ -48,6 +48,7 @@ constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kXcds = 8;
+constexpr int kCus = 256;  // MI355X: 8 XCDs x 32 CUs
 constexpr int kABytes = kBM * kBK * 2;  // one stage of A: 16 KB
 constexpr int kBBytes = kBN * kBK * 2;
 constexpr int kStageBytes = kABytes + kBBytes;
@@ -624,9 +625,11 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
     // anyway: split until the grid covers most CUs, keeping >= 8 K steps
     // per split for the DMA ring to overlap, or >= 4 while the grid stays
     // within half the CUs (small M, where more work-groups pulling operands
-    // win over a full ring).
+    // win over a full ring). Never past one work-group per CU: a second
+    // round of work-groups costs more than the longer K loop of fewer
+    // splits.
     for (const int s : {2, 3, 4, 6, 8}) {
-      if (plan.tiles * splits >= 160)
+      if (plan.tiles * splits >= 160 || plan.tiles * s > kCus)
         break;
       const int min_steps = plan.tiles * s <= 128 ? 4 : 8;
       if (k_steps % s == 0 && k_steps / s >= min_steps)

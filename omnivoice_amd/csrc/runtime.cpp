@@ -218,7 +218,7 @@ class Engine {
   std::int64_t GenerateTrace(const Input& in, const ovg_decoding& d,
                              std::uint64_t seed, std::int32_t* codes,
                              std::int32_t* unmasked_at, float* trace);
-  void Profile(const Input& in, std::int64_t repeats,
+  void Profile(const std::vector<Input>& items, std::int64_t repeats,
                std::map<std::string, KernelStat>* stats);
 
  private:
@@ -1090,13 +1090,13 @@ std::int64_t Engine::GenerateTrace(const Input& in, const ovg_decoding& d,
   return static_cast<std::int64_t>(launch_steps.size());
 }
 
-void Engine::Profile(const Input& in, std::int64_t repeats,
+void Engine::Profile(const std::vector<Input>& items, std::int64_t repeats,
                      std::map<std::string, KernelStat>* stats) {
-  const Layout L = Plan({in});
+  const Layout L = Plan(items);
   Prepare(L);
   ovg_decoding d{32, 2.0F, 0.1F, 5.0F, 0.0F};
   std::vector<int> launch_steps;
-  UploadDecodingPlan(L, d, {0}, &launch_steps);
+  UploadDecodingPlan(L, d, std::vector<std::uint64_t>(items.size(), 0), &launch_steps);
   for (std::int64_t r = 0; r < std::max<std::int64_t>(repeats, 1); ++r) {
     LaunchFill(codes_.get(), static_cast<int>(cfg_.audio_mask_id), L.outputs,
                stream_);
@@ -1306,14 +1306,19 @@ int ovg_generate_trace(ovg_handle* handle, const ovg_input* input,
   });
 }
 
-int ovg_profile_step(ovg_handle* handle, const ovg_input* input,
-                     int64_t repeats, ovg_kernel_stat* stats,
-                     int64_t capacity, int64_t* count, char* error,
-                     size_t error_len) {
+int ovg_profile_batch(ovg_handle* handle, int64_t items,
+                      const ovg_input* inputs, int64_t repeats,
+                      ovg_kernel_stat* stats, int64_t capacity, int64_t* count,
+                      char* error, size_t error_len) {
   return Guard("OmniVoice profile: ", error, error_len, [&] {
-    ovg::Require(handle != nullptr && count != nullptr, "null argument");
+    ovg::Require(handle != nullptr && count != nullptr && inputs != nullptr &&
+                     items > 0,
+                 "null argument");
+    std::vector<ovg::Input> list;
+    for (int64_t i = 0; i < items; ++i)
+      list.push_back(ToInput(&inputs[i]));
     std::map<std::string, ovg::KernelStat> table;
-    handle->engine->Profile(ToInput(input), repeats, &table);
+    handle->engine->Profile(list, repeats, &table);
     int64_t n = 0;
     for (const auto& [name, s] : table) {
       if (n < capacity && stats != nullptr) {
@@ -1330,6 +1335,14 @@ int ovg_profile_step(ovg_handle* handle, const ovg_input* input,
     *count = n;
     return OVG_OK;
   });
+}
+
+int ovg_profile_step(ovg_handle* handle, const ovg_input* input,
+                     int64_t repeats, ovg_kernel_stat* stats,
+                     int64_t capacity, int64_t* count, char* error,
+                     size_t error_len) {
+  return ovg_profile_batch(handle, 1, input, repeats, stats, capacity, count,
+                           error, error_len);
 }
 
 void ovg_synthetic_values(uint64_t weight_seed, uint64_t tensor, uint64_t first,

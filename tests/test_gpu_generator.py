@@ -202,6 +202,22 @@ def test_batch_matches_single_items(tiny):
         assert agree > 0.9, agree
 
 
+def test_profile_batch_counts_every_packed_row(tiny):
+    """The per-kernel profile of two identical items packed as one batch
+    has the same kernels and launch counts as one item, and twice its GEMM
+    work (the FLOP count follows the packed rows)."""
+    cfg, gen, _ = tiny
+    rng = np.random.default_rng(8)
+    it = inp(random_input(rng, cfg, 7, 0, 33), 7, 33)
+    one = gen.profile(it, repeats=1)
+    two = gen.profile([it, it], repeats=1)
+    assert set(one) == set(two)
+    for name, s in one.items():
+        assert two[name]["launches"] == s["launches"], name
+        if name.startswith("gemm_"):
+            assert two[name]["flops"] == pytest.approx(2 * s["flops"]), name
+
+
 # ------------------------------------------------------------------ released shape
 
 @pytest.fixture(scope="module")
@@ -240,3 +256,21 @@ def test_released_generate_properties(released, shape):
     assert ((a.codes >= 0) & (a.codes < 1024)).all()
     for step, count in enumerate(ov.unmask_schedule(8 * target, 32, 0.1)):
         assert (a.unmasked_at == step).sum() == count
+
+
+def test_released_chunk_batch_properties(released):
+    """Two 15 s chunks of long text (110 text tokens, 375 frames each) as one
+    batch: every item keeps its own schedule, and repeated runs agree."""
+    cfg, gen, _ = released
+    rng = np.random.default_rng(110)
+    items = [inp(random_input(rng, cfg, 110, 0, 375), 110, 375) for _ in range(2)]
+    dec = ov.DecodingConfig()
+    a = gen.generate_batch(items, dec, seeds=[42, 43])
+    b = gen.generate_batch(items, dec, seeds=[42, 43])
+    schedule = ov.unmask_schedule(8 * 375, 32, 0.1)
+    for ra, rb in zip(a, b):
+        np.testing.assert_array_equal(ra.codes, rb.codes)
+        np.testing.assert_array_equal(ra.unmasked_at, rb.unmasked_at)
+        assert ((ra.codes >= 0) & (ra.codes < 1024)).all()
+        for step, count in enumerate(schedule):
+            assert (ra.unmasked_at == step).sum() == count

@@ -35,6 +35,12 @@ class OrcConfig(ctypes.Structure):
                 ("audio_vocab_size", _i64), ("audio_mask_id", _u32)]
 
 
+class OrcCodecConfig(ctypes.Structure):
+    _fields_ = [("codebooks", _i64), ("codebook_size", _i64),
+                ("codebook_dim", _i64), ("hidden", _i64), ("latent", _i64),
+                ("channels", _i64), ("blocks", _i64), ("ratios", _i64 * 8)]
+
+
 def build(reference: bool = True) -> None:
     """Compiles liboracle.so and, when the reference tree is present,
     _ref/libref_decoding.so."""
@@ -87,6 +93,14 @@ def lib() -> ctypes.CDLL:
         "orc_qk_norm_rope": (None, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
                                     _f32, _f32]),
         "orc_attention": (None, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, ctypes.c_int]),
+        "orc_snake": (None, [_ptr, _i64, _i64, _ptr, _ptr]),
+        "orc_conv1d": (None, [_ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr]),
+        "orc_conv_transpose1d": (None, [_ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _ptr]),
+        "orc_codec_values": (None, [_u64, _u64, _u64, _i64, ctypes.c_double, ctypes.c_int,
+                                    _ptr]),
+        "orc_codec_synthetic": (_ptr, [ctypes.POINTER(OrcCodecConfig), _u64]),
+        "orc_codec_destroy": (None, [_ptr]),
+        "orc_codec_decode": (_i64, [_ptr, _ptr, _i64, _ptr]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -267,3 +281,82 @@ def released_config(vocab_size: int = 151936) -> dict:
                 layers=28, heads=16, kv_heads=8, head_dim=128,
                 max_positions=40960, rms_norm_eps=1e-6, rope_theta=1e6,
                 audio_codebooks=8, audio_vocab_size=1025, audio_mask_id=1024)
+
+
+# ------------------------------------------------------------------ codec
+
+def codec_released_config() -> dict:
+    """The audio tokenizer's decoder dimensions (tests/config_samples.hpp:34-70
+    of the reference): 8 codebooks of 1024 x 64, RVQ output 768 + 256, fc2 to
+    256 latent channels, 1024 decoder channels, upsampling 8, 5, 4, 2, 3
+    (960 samples per frame)."""
+    return dict(codebooks=8, codebook_size=1024, codebook_dim=64, hidden=1024,
+                latent=256, channels=1024, ratios=[8, 5, 4, 2, 3])
+
+
+def codec_config_struct(cfg: dict) -> OrcCodecConfig:
+    ratios = (_i64 * 8)(*cfg["ratios"])
+    return OrcCodecConfig(cfg["codebooks"], cfg["codebook_size"],
+                          cfg["codebook_dim"], cfg["hidden"], cfg["latent"],
+                          cfg["channels"], len(cfg["ratios"]), ratios)
+
+
+def snake(x: np.ndarray, alpha: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    alpha = np.ascontiguousarray(alpha, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_snake(_p(x), x.shape[0], x.shape[1], _p(alpha), _p(y))
+    return y
+
+
+def conv1d(x, w, b, dilation=1) -> np.ndarray:
+    """x [in][L], w [out][in][k]: nn.Conv1d, 'same' padding."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out, cin, k = w.shape
+    y = np.empty((out, x.shape[1]), dtype=np.float32)
+    lib().orc_conv1d(_p(x), cin, x.shape[1], _p(w), _p(b), out, k, dilation, _p(y))
+    return y
+
+
+def conv_transpose1d(x, w, b, stride) -> np.ndarray:
+    """x [in][L], w [in][out][2 stride]: the decoder's upsampling layer."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    cin, out, _ = w.shape
+    y = np.empty((out, x.shape[1] * stride), dtype=np.float32)
+    lib().orc_conv_transpose1d(_p(x), cin, x.shape[1], _p(w), _p(b), out, stride,
+                               _p(y))
+    return y
+
+
+def codec_values(seed, tensor, count, scale, exponential=False, first=0):
+    out = np.empty(count, dtype=np.float32)
+    lib().orc_codec_values(seed, tensor, first, count, scale, int(exponential),
+                           _p(out))
+    return out
+
+
+class Codec:
+    """The CPU audio decoder with synthetic (seeded) weights."""
+
+    def __init__(self, cfg: dict, seed: int = 1234):
+        self.cfg = dict(cfg)
+        self._c = codec_config_struct(cfg)
+        self._h = lib().orc_codec_synthetic(ctypes.byref(self._c), seed)
+
+    def decode(self, codes: np.ndarray) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        frames = codes.shape[1]
+        audio = np.empty(frames * int(np.prod(self.cfg["ratios"])), dtype=np.float32)
+        n = lib().orc_codec_decode(self._h, _p(codes), frames, _p(audio))
+        assert n == audio.size
+        return audio
+
+    def __del__(self):
+        try:
+            lib().orc_codec_destroy(self._h)
+        except Exception:
+            pass

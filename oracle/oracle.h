@@ -19,6 +19,13 @@
  *   orc_forward pieces   - float64 textbook formulas at tiny shapes and the
  *                          installed transformers Qwen3 layer (fixtures).
  *   orc_synth_*          - numpy float16 rounding; closed-form moments.
+ *   orc_conv1d, orc_conv_transpose1d, orc_snake
+ *                        - torch.nn.functional.conv1d / conv_transpose1d
+ *                          in float64 on the CPU, and the Snake closed form.
+ *   orc_codec_decode     - the same composition of torch float64 layers at
+ *                          a small configuration; the real-checkpoint decode
+ *                          vectors of the reference fixture need the codec
+ *                          weights, which are absent (parity unpinned there).
  */
 #ifndef OMNIVOICE_ORACLE_H_
 #define OMNIVOICE_ORACLE_H_
@@ -111,6 +118,34 @@ void orc_qk_norm_rope(const float* qkv, const float* q_norm,
 void orc_attention(const float* qkv, float* out, int64_t rows, int64_t heads,
                    int64_t kv_heads, int64_t head_dim,
                    const int64_t* sequences, int64_t count, int round_p);
+
+/* codec.cpp: the audio decoder (codec.cpp:197-260 of the reference) */
+typedef struct orc_codec_config {
+  int64_t codebooks, codebook_size, codebook_dim;
+  int64_t hidden;    /* semantic hidden + latent: the RVQ output width */
+  int64_t latent;    /* fc2 output channels */
+  int64_t channels;  /* decoder channels before the first block */
+  int64_t blocks;
+  int64_t ratios[8]; /* upsampling ratio per block */
+} orc_codec_config;
+void orc_snake(const float* x, int64_t channels, int64_t length,
+               const float* alpha, float* y);
+/* w [out][in][kernel], padding (kernel - 1) dilation / 2 */
+void orc_conv1d(const float* x, int64_t in, int64_t length, const float* w,
+                const float* b, int64_t out, int64_t kernel, int64_t dilation,
+                float* y);
+/* w [in][out][2 stride], padding ceil(stride / 2), output_padding stride % 2 */
+void orc_conv_transpose1d(const float* x, int64_t in, int64_t length,
+                          const float* w, const float* b, int64_t out,
+                          int64_t stride, float* y);
+void orc_codec_values(uint64_t seed, uint64_t tensor, uint64_t first,
+                      int64_t count, double scale, int exponential,
+                      float* out);
+void* orc_codec_synthetic(const orc_codec_config* config, uint64_t seed);
+void orc_codec_destroy(void* codec);
+/* codes [codebooks][frames]; audio receives the returned sample count */
+int64_t orc_codec_decode(const void* codec, const int32_t* codes,
+                         int64_t frames, float* audio);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,12 @@ class _KernelStat(ctypes.Structure):
                 ("bytes", ctypes.c_double)]
 
 
+class _CodecConfig(ctypes.Structure):
+    _fields_ = [("codebooks", _i64), ("codebook_size", _i64), ("codebook_dim", _i64),
+                ("hidden", _i64), ("latent", _i64), ("channels", _i64),
+                ("blocks", _i64), ("ratios", _i64 * 8)]
+
+
 _CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
 
 EXPORTS = {
@@ -112,6 +118,21 @@ EXPORTS = {
                                       _sz]),
     "ovg_op_attention": (ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i64, _ptr, _i64,
                                         _ptr, _err, _sz]),
+    # the audio decoder (include/omnivoice_codec_mi355x.h)
+    "ovc_create": (ctypes.c_int, [ctypes.POINTER(_CodecConfig), ctypes.c_char_p, _u64,
+                                  ctypes.POINTER(_ptr), _err, _sz]),
+    "ovc_destroy": (None, [_ptr]),
+    "ovc_samples": (_i64, [_ptr, _i64]),
+    "ovc_decode": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _err, _sz]),
+    "ovc_decode_device": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _ptr, _err, _sz]),
+    "ovc_profile_decode": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _i64,
+                                          ctypes.POINTER(_i64), _err, _sz]),
+    "ovc_synthetic_values": (None, [_u64, _u64, _u64, _i64, ctypes.c_double, ctypes.c_int,
+                                    _ptr]),
+    "ovc_op_conv1d": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64,
+                                     ctypes.c_int, _ptr, _ptr, _err, _sz]),
+    "ovc_op_conv_transpose1d": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64,
+                                               _i64, _ptr, _ptr, _err, _sz]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -473,3 +494,127 @@ def op_attention(qkv, out, heads: int, kv_heads: int,
     _check(lib().ovg_op_attention(_dev(qkv), _dev(out), rows, heads, kv_heads,
                                   _p(seq), len(sequences), _stream(stream),
                                   err, len(err)), err)
+
+
+# --------------------------------------------------------------- audio decoder
+
+def codec_released_config() -> dict:
+    """The released audio tokenizer's decoder (tests/config_samples.hpp:34-70
+    of the reference): 8 codebooks of 1024 x 64, RVQ output 768 + 256, fc2 to
+    256 latent channels, 1024 decoder channels, upsampling 8, 5, 4, 2, 3
+    (960 samples per frame at 24 kHz)."""
+    return dict(codebooks=8, codebook_size=1024, codebook_dim=64, hidden=1024,
+                latent=256, channels=1024, ratios=[8, 5, 4, 2, 3])
+
+
+def _codec_config(cfg: dict) -> _CodecConfig:
+    ratios = list(cfg["ratios"])
+    return _CodecConfig(cfg["codebooks"], cfg["codebook_size"], cfg["codebook_dim"],
+                        cfg["hidden"], cfg["latent"], cfg["channels"], len(ratios),
+                        (_i64 * 8)(*ratios))
+
+
+def codec_synthetic_values(seed: int, tensor: int, first: int, count: int,
+                           scale: float, exponential: bool = False) -> np.ndarray:
+    out = np.zeros(count, dtype=np.float32)
+    lib().ovc_synthetic_values(seed, tensor, first, count, scale, int(exponential),
+                               _p(out))
+    return out
+
+
+class Codec:
+    """The audio tokenizer's decoder on the GPU: codes [codebooks][frames] to
+    24 kHz float32 audio (codec.hpp:16-45 of the reference, Decode). Not
+    thread-safe."""
+
+    def __init__(self, handle: int, cfg: dict):
+        self._h = handle
+        self.cfg = dict(cfg)
+
+    @classmethod
+    def load(cls, cfg: dict, model_root: Optional[str] = None,
+             seed: int = 1234) -> "Codec":
+        """model_root/audio_tokenizer/model.safetensors, or the seeded
+        synthetic decoder when model_root is None."""
+        c = _codec_config(cfg)
+        h = _ptr()
+        err = _buf()
+        root = model_root.encode() if model_root else None
+        _check(lib().ovc_create(ctypes.byref(c), root, seed, ctypes.byref(h), err,
+                                len(err)), err)
+        return cls(h.value, cfg)
+
+    @classmethod
+    def synthetic(cls, cfg: dict, seed: int = 1234) -> "Codec":
+        return cls.load(cfg, None, seed)
+
+    def samples(self, frames: int) -> int:
+        return int(lib().ovc_samples(self._h, frames))
+
+    def decode(self, codes) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, dtype=np.int32)
+        frames = codes.shape[1]
+        audio = np.zeros(self.samples(frames), dtype=np.float32)
+        err = _buf()
+        _check(lib().ovc_decode(self._h, _p(codes), frames, _p(audio), err, len(err)),
+               err)
+        return audio
+
+    def decode_device(self, codes, audio, stream=None) -> None:
+        """codes: int32 device tensor [codebooks][frames]; audio: float32
+        device tensor of samples(frames). Enqueued on `stream`."""
+        err = _buf()
+        _check(lib().ovc_decode_device(self._h, _dev(codes), codes.shape[1], _dev(audio),
+                                       _stream(stream), err, len(err)), err)
+
+    def profile(self, frames: int, repeats: int = 3) -> dict:
+        cap = 32
+        stats = (_KernelStat * cap)()
+        count = _i64()
+        err = _buf()
+        _check(lib().ovc_profile_decode(self._h, frames, repeats, ctypes.cast(stats, _ptr),
+                                        cap, ctypes.byref(count), err, len(err)), err)
+        out = {}
+        for i in range(min(count.value, cap)):
+            s = stats[i]
+            out[s.name.decode()] = dict(launches=s.launches, total_ms=s.total_ms,
+                                        flops=s.flops, bytes=s.bytes)
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            lib().ovc_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def op_conv1d(x, w, b, y, alpha=None, dilation: int = 1, accumulate: bool = False,
+              stream=None) -> None:
+    """x [in][L], y [out][L], alpha [in]: float32 device tensors; w [out][in][k]
+    and b [out]: host float32 arrays."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out, cin, k = w.shape
+    err = _buf()
+    _check(lib().ovc_op_conv1d(_dev(x), cin, x.shape[1],
+                               _dev(alpha) if alpha is not None else None, _p(w), _p(b),
+                               out, k, dilation, int(accumulate), _dev(y), _stream(stream),
+                               err, len(err)), err)
+
+
+def op_conv_transpose1d(x, w, b, y, stride: int, alpha=None, stream=None) -> None:
+    """x [in][L], y [out][L stride], alpha [in]: float32 device tensors;
+    w [in][out][2 stride] and b [out]: host float32 arrays."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    cin, out, _ = w.shape
+    err = _buf()
+    _check(lib().ovc_op_conv_transpose1d(_dev(x), cin, x.shape[1],
+                                         _dev(alpha) if alpha is not None else None,
+                                         _p(w), _p(b), out, stride, _dev(y),
+                                         _stream(stream), err, len(err)), err)

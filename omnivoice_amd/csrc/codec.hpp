@@ -1,0 +1,65 @@
+// Launchers of the audio decoder's gfx950 kernels (codec_kernels.hip).
+// Signals are float32, channel-major: [channels][samples].
+#ifndef OMNIVOICE_AMD_CODEC_HPP_
+#define OMNIVOICE_AMD_CODEC_HPP_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ovg {
+
+constexpr int kConvMaxTaps = 7;
+constexpr int kConvMaxPhases = 8;
+// Largest spread between a convolution's first and last tap (kernel 7 at
+// dilation 9 spans 54 samples).
+constexpr int kConvMaxSpan = 64;
+
+// One convolution as an implicit GEMM on the fp32 matrix cores:
+//   y[o][m * out_stride + phase] (+)= bias[o] + sum_{k, i}
+//       w[phase][k][i][o] * act(x[i][m + offsets[phase][k]])
+// for output positions m < positions, with x = 0 outside [0, len_in) and
+// act the Snake activation x + sin^2(alpha_i x) / (alpha_i + 1e-9) when
+// `alpha` is set (the identity otherwise). A Conv1d is one phase with taps
+// at k dilation - pad; a ConvTranspose1d of stride s is s phases of two taps
+// each (see the codec engine).
+struct ConvParams {
+  const float* x;      // [cin][len_in]
+  const float* alpha;  // [cin] or null
+  const float* w;      // [phases][taps][cin][cout]
+  const float* bias;   // [cout]
+  float* y;            // [cout][len_out]
+  int cin, len_in, cout, len_out;
+  int taps, phases, positions, out_stride;
+  int accumulate;  // y += result instead of y = result
+  int offsets[kConvMaxPhases][kConvMaxTaps];
+};
+void LaunchConv(const ConvParams& p, hipStream_t stream);
+
+// The decoder's last layer, one output channel: y[t] = bias + sum_{k, i}
+// w[k][i] act(x[i][t + k - pad]), pad = (taps - 1) / 2.
+struct OutputConvParams {
+  const float* x;      // [cin][length]
+  const float* alpha;  // [cin]
+  const float* w;      // [taps][cin]
+  const float* bias;   // [1]
+  float* y;            // [length]
+  int cin, length, taps;
+};
+void LaunchOutputConv(const OutputConvParams& p, hipStream_t stream);
+
+// RVQ decode folded with fc2: y[o][f] = bias[o] + sum_c
+// table[c][codes[c][f]][o], i.e. the latent input of the decoder, channel
+// major.
+struct RvqParams {
+  const float* table;  // [codebooks][entries][latent]
+  const float* bias;   // [latent]
+  const std::int32_t* codes;  // [codebooks][frames]
+  float* y;            // [latent][frames]
+  int codebooks, entries, latent, frames;
+};
+void LaunchRvq(const RvqParams& p, hipStream_t stream);
+
+}  // namespace ovg
+
+#endif  // OMNIVOICE_AMD_CODEC_HPP_

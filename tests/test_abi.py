@@ -15,15 +15,18 @@ from conftest import ROOT
 
 
 def declared_functions():
-    with open(os.path.join(ROOT, "include", "omnivoice_mi355x.h")) as f:
-        text = f.read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ovg_\w+)\s*\(", text)))
+    names = set()
+    for header in ("omnivoice_mi355x.h", "omnivoice_codec_mi355x.h"):
+        with open(os.path.join(ROOT, "include", header)) as f:
+            text = f.read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(ov[gc]_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
     names = declared_functions()
-    assert len(names) >= 19
+    assert len(names) >= 28
     lib = ctypes.CDLL(ov.LIB_PATH)
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -80,3 +83,17 @@ def test_build_input_rejects_bad_arguments():
     ids = np.zeros(8, dtype=np.int32)
     assert ov.lib().ovg_build_input(None, -1, None, 0, 1, 8, 1024,
                                     ids.ctypes.data) == -1
+
+
+def test_codec_config_and_file_errors_before_the_gpu():
+    """Configuration and checkpoint errors are reported with the reference's
+    prefix before any device work (codec.cpp:143-145)."""
+    cfg = ov.codec_released_config()
+    with pytest.raises(ov.GeneratorError,
+                       match="^OmniVoice audio tokenizer: config: 1 to 8 upsampling blocks"):
+        ov.Codec.load(dict(cfg, ratios=[]))
+    with pytest.raises(ov.GeneratorError, match="can't be halved"):
+        ov.Codec.load(dict(cfg, channels=1000))
+    with pytest.raises(ov.GeneratorError,
+                       match="^OmniVoice audio tokenizer: .*audio_tokenizer/model.safetensors"):
+        ov.Codec.load(cfg, "/nonexistent")

@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 WORKLOADS = {
@@ -83,6 +84,71 @@ def cpu_baseline(cfg, x, decoding, steps):
             "utterance_rtf_extrapolated": (elapsed / steps * 32) / (F / 25.0)}
 
 
+def bench_codec(args, torch):
+    """The audio decoder on the workload's frames: codes resident on the
+    device, audio left there (Codec::Decode without the host copies)."""
+    import omnivoice_amd as ov
+    cfg = ov.codec_released_config()
+    frames = WORKLOADS[args.workload][2] * ITEMS.get(args.workload, 1)
+    codec = ov.Codec.synthetic(cfg, 1234)
+    rng = np.random.default_rng(42)
+    codes_host = rng.integers(0, 1024, size=(8, frames)).astype(np.int32)
+    codes = torch.from_numpy(codes_host).cuda()
+    audio = torch.empty(codec.samples(frames), dtype=torch.float32, device="cuda")
+    for _ in range(args.warmup):
+        codec.decode_device(codes, audio)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        codec.decode_device(codes, audio)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    seconds = frames / 25.0
+    stats = codec.profile(frames, repeats=args.profile_repeats)
+    kernels = {n: {"launches": s["launches"], "avg_us": s["total_ms"] / s["launches"] * 1e3,
+                   "tflops": s["flops"] / (s["total_ms"] * 1e-3) / 1e12 if s["flops"] else None}
+               for n, s in stats.items()}
+    dominant = max(stats, key=lambda n: stats[n]["total_ms"])
+    d = stats[dominant]
+    achieved = d["flops"] / (d["total_ms"] * 1e-3) / 1e12
+    total_flops = sum(s["flops"] for s in stats.values()) / args.profile_repeats
+    result = {
+        "metric": f"audio decode, {seconds:g} s of 24 kHz audio ({frames} frames), 1 GPU",
+        "value": seconds * args.steps / elapsed,
+        "unit": "audio seconds decoded per second",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded decoder weights, uniform codes)",
+        "config": {"workload": f"{args.workload}: decode of {frames} frames x 8 codebooks "
+                               f"to {codec.samples(frames)} samples",
+                   "decoder": "Higgs Audio v2 DAC decoder (1024 ch, upsampling 8 5 4 2 3)",
+                   "parallelism": "single GPU"},
+        "decode_rtf": (elapsed / args.steps) / seconds,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "kernel": dominant,
+                     "avg_launch_us": d["total_ms"] / d["launches"] * 1e3},
+        "decode_tflops": total_flops / (elapsed / args.steps) / 1e12,
+        "kernels": kernels,
+    }
+    if args.cpu_steps > 0:
+        import oracle
+        threads = min(16, os.cpu_count() or 1)
+        oracle.lib().orc_set_threads(threads)
+        model = oracle.Codec(oracle.codec_released_config(), 1234)
+        sample = codes_host[:, :25]
+        t0 = time.perf_counter()
+        model.decode(sample)
+        cpu = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": 1.0 / cpu, "unit": "audio seconds decoded per second",
+                                  "cores": threads, "kind": "port",
+                                  "sample": "1 s (25 frames) decoded by the float32 oracle "
+                                            "(double sums); table synthesis excluded"}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +158,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=2,
                     help="unmasking steps timed for the CPU baseline (0 skips it)")
     ap.add_argument("--profile-repeats", type=int, default=3)
+    ap.add_argument("--codec", action="store_true",
+                    help="benchmark the audio decoder on the workload's frames instead")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only copy this many MiB device to device 3 times (a "
                          "copy kernel of known size for calibrating memory "
@@ -113,6 +181,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": n, "copies": 3}), flush=True)
+        return
+    if args.codec:
+        bench_codec(args, torch)
         return
     import omnivoice_amd as ov
 

@@ -184,8 +184,9 @@ class CodecEngine {
   void Reserve(std::int64_t frames);
   void Enqueue(const std::int32_t* codes, std::int64_t frames, float* audio,
                hipStream_t stream, Profiler* prof);
-  void RunConv(const Conv& c, const float* x, const float* alpha, int length, float* y,
-               bool accumulate, hipStream_t stream, Profiler* prof, const char* name);
+  void RunConv(const Conv& c, const float* x, int length, float* y, float* y_act,
+               const float* alpha_out, bool accumulate, hipStream_t stream, Profiler* prof,
+               const char* name);
 
   ovc_config cfg_;
   std::int64_t hop_ = 1;
@@ -193,8 +194,10 @@ class CodecEngine {
   DeviceBuffer<float> table_, fc2_bias_, final_alpha_, out_w_, out_b_;
   Conv input_;
   std::vector<std::unique_ptr<Block>> blocks_;
-  // Work buffers: the latent input, two signals and the residual branch.
-  DeviceBuffer<float> latent_, a_, b_, y_, audio_;
+  // Work buffers: the latent input, the signal, its Snake-activated copies
+  // (the next convolution's input; two, so that an upsampling layer reads
+  // one and writes the other) and the residual branch's activated output.
+  DeviceBuffer<float> latent_, x_, xa_[2], ya_, audio_;
   DeviceBuffer<std::int32_t> codes_;
   std::int64_t reserved_ = 0;
 };
@@ -300,23 +303,25 @@ void CodecEngine::Reserve(std::int64_t frames) {
   // 2^31 samples per channel and elements in all.
   Require(largest < (std::int64_t{1} << 31), "too many frames");
   latent_.Reserve(static_cast<std::size_t>(cfg_.latent * frames));
-  a_.Reserve(static_cast<std::size_t>(largest));
-  b_.Reserve(static_cast<std::size_t>(largest));
-  y_.Reserve(static_cast<std::size_t>(largest));
+  x_.Reserve(static_cast<std::size_t>(largest));
+  xa_[0].Reserve(static_cast<std::size_t>(largest));
+  xa_[1].Reserve(static_cast<std::size_t>(largest));
+  ya_.Reserve(static_cast<std::size_t>(largest));
   audio_.Reserve(static_cast<std::size_t>(length));
   codes_.Reserve(static_cast<std::size_t>(cfg_.codebooks * frames));
   reserved_ = frames;
 }
 
-void CodecEngine::RunConv(const Conv& c, const float* x, const float* alpha, int length,
-                          float* y, bool accumulate, hipStream_t stream, Profiler* prof,
-                          const char* name) {
+void CodecEngine::RunConv(const Conv& c, const float* x, int length, float* y, float* y_act,
+                          const float* alpha_out, bool accumulate, hipStream_t stream,
+                          Profiler* prof, const char* name) {
   ConvParams p{};
   p.x = x;
-  p.alpha = alpha;
   p.w = c.w.get();
   p.bias = c.b.get();
   p.y = y;
+  p.y_act = y_act;
+  p.alpha_out = alpha_out;
   p.cin = c.in;
   p.len_in = length;
   p.cout = c.out;
@@ -330,8 +335,9 @@ void CodecEngine::RunConv(const Conv& c, const float* x, const float* alpha, int
   for (int k = 0; k < c.taps; ++k)
     p.offsets[0][k] = k * c.dilation - pad;
   const double flops = 2.0 * c.out * static_cast<double>(length) * c.in * c.taps;
-  const double bytes = 4.0 * length * (c.in + c.out * (accumulate ? 2.0 : 1.0)) +
-                       4.0 * c.taps * c.in * c.out;
+  const double outputs = (y != nullptr ? 1.0 : 0.0) + (y_act != nullptr ? 1.0 : 0.0) +
+                         (accumulate ? 1.0 : 0.0);
+  const double bytes = 4.0 * length * (c.in + c.out * outputs) + 4.0 * c.taps * c.in * c.out;
   auto launch = [&] { LaunchConv(p, stream); };
   if (prof != nullptr)
     prof->Run(name, flops, bytes, launch);
@@ -361,49 +367,60 @@ void CodecEngine::Enqueue(const std::int32_t* codes, std::int64_t frames, float*
   r.frames = F;
   run("codec_rvq", 0.0, 4.0 * cfg_.codebooks * cfg_.latent * F * 2.0,
       [&] { LaunchRvq(r, stream); });
-  RunConv(input_, latent_.get(), nullptr, F, a_.get(), false, stream, prof, "codec_conv_in");
-  float* cur = a_.get();
-  float* next = b_.get();
+  // Every Snake is computed once, by the epilogue of the convolution that
+  // produces its input: xa holds snake(x) with the alpha of whatever reads
+  // it next, ya the residual branch's snake(conv1(...)).
+  const float* first_alpha =
+      blocks_.empty() ? final_alpha_.get() : blocks_.front()->alpha.get();
+  int cur = 0;
+  RunConv(input_, latent_.get(), F, nullptr, xa_[cur].get(), first_alpha, false, stream, prof,
+          "codec_conv_in");
   int length = F;
-  for (const auto& blk : blocks_) {
-    // Snake + transposed convolution (codec_state.hpp:272-288).
+  for (std::size_t bi = 0; bi < blocks_.size(); ++bi) {
+    const Block& blk = *blocks_[bi];
+    // Transposed convolution (codec_state.hpp:272-288) of snake(x): the raw
+    // output is the new signal, its Snake feeds the first residual unit.
     ConvParams p{};
-    p.x = cur;
-    p.alpha = blk->alpha.get();
-    p.w = blk->w.get();
-    p.bias = blk->b.get();
-    p.y = next;
-    p.cin = blk->in;
+    p.x = xa_[cur].get();
+    p.w = blk.w.get();
+    p.bias = blk.b.get();
+    p.y = x_.get();
+    p.y_act = xa_[1 - cur].get();
+    p.alpha_out = blk.units[0].alpha1.get();
+    p.cin = blk.in;
     p.len_in = length;
-    p.cout = blk->out;
-    p.len_out = length * blk->stride;
+    p.cout = blk.out;
+    p.len_out = length * blk.stride;
     p.taps = 2;
-    p.phases = blk->stride;
+    p.phases = blk.stride;
     p.positions = length;
-    p.out_stride = blk->stride;
-    const UpsampleTaps u = Phases(blk->stride);
-    for (int ph = 0; ph < blk->stride; ++ph)
+    p.out_stride = blk.stride;
+    const UpsampleTaps u = Phases(blk.stride);
+    for (int ph = 0; ph < blk.stride; ++ph)
       for (int k = 0; k < 2; ++k)
         p.offsets[ph][k] = u.offsets[ph][k];
-    run("codec_upsample", 2.0 * blk->out * double(length) * blk->stride * blk->in * 2,
-        4.0 * length * (blk->in + blk->out * double(blk->stride)) +
-            4.0 * 2 * blk->stride * blk->in * blk->out,
+    run("codec_upsample", 2.0 * blk.out * double(length) * blk.stride * blk.in * 2,
+        4.0 * length * (blk.in + 2.0 * blk.out * blk.stride) +
+            4.0 * 2 * blk.stride * blk.in * blk.out,
         [&] { LaunchConv(p, stream); });
-    length *= blk->stride;
-    // Residual units (codec_state.hpp:252-270): y = conv1(snake(x)),
-    // x += conv2(snake(y)).
-    for (const Unit& unit : blk->units) {
-      RunConv(unit.conv1, next, unit.alpha1.get(), length, y_.get(), false, stream, prof,
-              "codec_res_conv7");
-      RunConv(unit.conv2, y_.get(), unit.alpha2.get(), length, next, true, stream, prof,
-              "codec_res_conv1");
+    cur = 1 - cur;
+    length *= blk.stride;
+    // Residual units (codec_state.hpp:252-270): x += conv2(snake(conv1(snake(x)))).
+    for (int ui = 0; ui < 3; ++ui) {
+      const Unit& unit = blk.units[ui];
+      const float* next_alpha = ui < 2 ? blk.units[ui + 1].alpha1.get()
+                                : bi + 1 < blocks_.size() ? blocks_[bi + 1]->alpha.get()
+                                                          : final_alpha_.get();
+      RunConv(unit.conv1, xa_[cur].get(), length, nullptr, ya_.get(), unit.alpha2.get(), false,
+              stream, prof, "codec_res_conv7");
+      RunConv(unit.conv2, ya_.get(), length, x_.get(), xa_[cur].get(), next_alpha, true, stream,
+              prof, "codec_res_conv1");
     }
-    std::swap(cur, next);
   }
-  // Final Snake and output convolution, no tanh (codec.cpp:244-251).
+  // Output convolution of snake(x), no tanh (codec.cpp:244-251).
   OutputConvParams o{};
-  o.x = cur;
-  o.alpha = final_alpha_.get();
+  o.x = xa_[cur].get();
+  o.alpha = nullptr;
   o.w = out_w_.get();
   o.bias = out_b_.get();
   o.y = audio;
@@ -590,7 +607,7 @@ int ovc_op_conv1d(const float* x, int64_t in, int64_t length, const float* alpha
     ovg::Upload(bd, std::vector<float>(b, b + O));
     ovg::ConvParams p{};
     p.x = x;
-    p.alpha = alpha;
+    p.alpha_in = alpha;
     p.w = wd.get();
     p.bias = bd.get();
     p.y = y;
@@ -631,7 +648,7 @@ int ovc_op_conv_transpose1d(const float* x, int64_t in, int64_t length, const fl
     ovg::Upload(bd, std::vector<float>(b, b + O));
     ovg::ConvParams p{};
     p.x = x;
-    p.alpha = alpha;
+    p.alpha_in = alpha;
     p.w = wd.get();
     p.bias = bd.get();
     p.y = y;

@@ -16,31 +16,35 @@ constexpr int kConvMaxPhases = 8;
 constexpr int kConvMaxSpan = 64;
 
 // One convolution as an implicit GEMM on the fp32 matrix cores:
-//   y[o][m * out_stride + phase] (+)= bias[o] + sum_{k, i}
-//       w[phase][k][i][o] * act(x[i][m + offsets[phase][k]])
-// for output positions m < positions, with x = 0 outside [0, len_in) and
-// act the Snake activation x + sin^2(alpha_i x) / (alpha_i + 1e-9) when
-// `alpha` is set (the identity otherwise). A Conv1d is one phase with taps
-// at k dilation - pad; a ConvTranspose1d of stride s is s phases of two taps
-// each (see the codec engine).
+//   v[o][t] = bias[o] + sum_{k, i} w[phase][k][i][o] * act_in(x[i][m + offsets[phase][k]])
+//   y[o][t] = v (or y += v), y_act[o][t] = act_out(y[o][t]),  t = m out_stride + phase
+// for output positions m < positions, with x = 0 outside [0, len_in), and
+// act the Snake activation x + sin^2(alpha x) / (alpha + 1e-9) of the
+// channel's alpha (act_in the identity when alpha_in is null). A Conv1d is
+// one phase with taps at k dilation - pad; a ConvTranspose1d of stride s is
+// s phases of two taps each (see the codec engine). Either output may be
+// null (y not with accumulate).
 struct ConvParams {
-  const float* x;      // [cin][len_in]
-  const float* alpha;  // [cin] or null
-  const float* w;      // [phases][taps][cin][cout]
-  const float* bias;   // [cout]
-  float* y;            // [cout][len_out]
+  const float* x;         // [cin][len_in]
+  const float* alpha_in;  // [cin] or null
+  const float* w;         // [phases][taps][cin][cout]
+  const float* bias;      // [cout]
+  float* y;               // [cout][len_out] or null
+  float* y_act;           // [cout][len_out] or null
+  const float* alpha_out; // [cout], with y_act
   int cin, len_in, cout, len_out;
   int taps, phases, positions, out_stride;
-  int accumulate;  // y += result instead of y = result
+  int accumulate;  // y += v instead of y = v
   int offsets[kConvMaxPhases][kConvMaxTaps];
 };
 void LaunchConv(const ConvParams& p, hipStream_t stream);
 
 // The decoder's last layer, one output channel: y[t] = bias + sum_{k, i}
-// w[k][i] act(x[i][t + k - pad]), pad = (taps - 1) / 2.
+// w[k][i] act(x[i][t + k - pad]), pad = (taps - 1) / 2, act the Snake of
+// `alpha` or the identity when it is null.
 struct OutputConvParams {
   const float* x;      // [cin][length]
-  const float* alpha;  // [cin]
+  const float* alpha;  // [cin] or null
   const float* w;      // [taps][cin]
   const float* bias;   // [1]
   float* y;            // [length]

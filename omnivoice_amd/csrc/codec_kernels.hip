@@ -31,11 +31,15 @@ __device__ __forceinline__ float Snake(float v, float a) {
   return v + (1.0F / (a + 1e-9F)) * (s * s);
 }
 
-template <int BM, int BN>
-__global__ __launch_bounds__(kThreads) void ConvKernel(ConvParams p) {
-  static_assert(BM * BN == 4 * 32 * 32, "four 32 x 32 wave blocks");
+template <int BM, int BN, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
+  static_assert(BM * BN == WAVES * 32 * 32, "one 32 x 32 block per wave");
+  constexpr int kT = 64 * WAVES;
   constexpr int kWavesN = BN / 32;
   constexpr int kWidth = BN + kConvMaxSpan;
+  constexpr int kXSlots = (kWidth + kT - 1) / kT;           // input columns per thread
+  constexpr int kWSlots = kConvMaxTaps * kChunk * BM / kT;  // weights per thread
+  static_assert(kConvMaxTaps * kChunk * BM % kT == 0, "weight slots");
   __shared__ float xs[kChunk][kWidth];
   __shared__ float ws[kConvMaxTaps][kChunk][BM];
 
@@ -57,67 +61,101 @@ __global__ __launch_bounds__(kThreads) void ConvKernel(ConvParams p) {
     hi = max(hi, offsets[k]);
   }
   const int width = BN + hi - lo;  // <= kWidth (checked by the launcher)
+  const int weights = taps * kChunk * BM;
   const float* w = p.w + static_cast<size_t>(phase) * taps * p.cin * p.cout;
 
-  floatx16 acc = {};
-  for (int c0 = 0; c0 < p.cin; c0 += kChunk) {
-    // The input window: xs[c][j] = act(x[c0 + c][m0 + lo + j]). Each thread
-    // takes whole columns, so a column's 16 loads leave together.
-    // Loads are unconditional (clamped addresses, then a select), so that
-    // all of them leave before the first returns.
-    for (int j = tid; j < width; j += kThreads) {
-      const int t = m0 + lo + j;
-      const bool inside = t >= 0 && t < p.len_in;
-      const int tc = min(max(t, 0), p.len_in - 1);
-      float v[kChunk];
+  // A chunk's operands pass through registers: fetch() issues the global
+  // loads of chunk c0 (unconditional, clamped addresses), stash() writes
+  // them to LDS with the input activation and the zero padding applied.
+  // The next chunk is fetched before the current chunk's MFMAs, so its
+  // loads are in flight while they run.
+  float xr[kXSlots][kChunk];
+  float wr[kWSlots];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int q = 0; q < kXSlots; ++q) {
+      const int t = min(max(m0 + lo + tid + q * kT, 0), p.len_in - 1);
 #pragma unroll
       for (int c = 0; c < kChunk; ++c)
-        v[c] = p.x[static_cast<size_t>(min(c0 + c, p.cin - 1)) * p.len_in + tc];
-      if (p.alpha != nullptr) {
-#pragma unroll
-        for (int c = 0; c < kChunk; ++c)
-          v[c] = Snake(v[c], p.alpha[min(c0 + c, p.cin - 1)]);
-      }
-#pragma unroll
-      for (int c = 0; c < kChunk; ++c)
-        xs[c][j] = inside && c0 + c < p.cin ? v[c] : 0.0F;
+        xr[q][c] = p.x[static_cast<size_t>(min(c0 + c, p.cin - 1)) * p.len_in + t];
     }
-    for (int i = tid; i < taps * kChunk * BM; i += kThreads) {
+#pragma unroll
+    for (int q = 0; q < kWSlots; ++q) {
+      const int i = tid + q * kT;
       const int o = i % BM;
       const int c = (i / BM) % kChunk;
-      const int k = i / (BM * kChunk);
-      const int ci = c0 + c;
-      const int co = co0 + o;
-      const float v = w[(static_cast<size_t>(k) * p.cin + min(ci, p.cin - 1)) * p.cout +
-                        min(co, p.cout - 1)];
-      ws[k][c][o] = ci < p.cin && co < p.cout ? v : 0.0F;
+      const int k = min(i / (BM * kChunk), taps - 1);
+      wr[q] = w[(static_cast<size_t>(k) * p.cin + min(c0 + c, p.cin - 1)) * p.cout +
+                min(co0 + o, p.cout - 1)];
     }
+  };
+  auto stash = [&](int c0) {
+#pragma unroll
+    for (int q = 0; q < kXSlots; ++q) {
+      const int j = tid + q * kT;
+      if (j < width) {
+        const int t = m0 + lo + j;
+        const bool inside = t >= 0 && t < p.len_in;
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c) {
+          float v = xr[q][c];
+          if (p.alpha_in != nullptr)
+            v = Snake(v, p.alpha_in[min(c0 + c, p.cin - 1)]);
+          xs[c][j] = inside && c0 + c < p.cin ? v : 0.0F;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kWSlots; ++q) {
+      const int i = tid + q * kT;
+      if (i < weights) {
+        const int o = i % BM;
+        const int c = (i / BM) % kChunk;
+        const int k = i / (BM * kChunk);
+        ws[k][c][o] = c0 + c < p.cin && co0 + o < p.cout ? wr[q] : 0.0F;
+      }
+    }
+  };
+
+  // Two accumulator chains (alternate channel pairs), so that consecutive
+  // MFMAs of a wave do not wait for each other.
+  floatx16 acc[2] = {};
+  fetch(0);
+  for (int c0 = 0; c0 < p.cin; c0 += kChunk) {
+    stash(c0);
     __syncthreads();
+    if (c0 + kChunk < p.cin)
+      fetch(c0 + kChunk);
     for (int k = 0; k < taps; ++k) {
       const int shift = offsets[k] - lo;
 #pragma unroll
       for (int s = 0; s < kChunk / 2; ++s) {
         const float a = ws[k][2 * s + half][row + l32];
         const float b = xs[2 * s + half][col + l32 + shift];
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+        acc[s & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[s & 1], 0, 0, 0);
       }
     }
     __syncthreads();
   }
 
-  // Element r of the accumulator: output channel row + 8 (r / 4) +
+  // Element r of the accumulators: output channel row + 8 (r / 4) +
   // 4 half + r % 4, position col + l32.
   const int m = m0 + col + l32;
   if (m >= p.positions)
     return;
-  float* out = p.y + static_cast<size_t>(m) * p.out_stride + phase;
+  const size_t t = static_cast<size_t>(m) * p.out_stride + phase;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int co = co0 + row + 8 * (r >> 2) + 4 * half + (r & 3);
     if (co < p.cout) {
-      float* dst = out + static_cast<size_t>(co) * p.len_out;
-      const float v = acc[r] + p.bias[co];
-      *dst = p.accumulate ? *dst + v : v;
+      const size_t at = static_cast<size_t>(co) * p.len_out + t;
+      float v = (acc[0][r] + acc[1][r]) + p.bias[co];
+      if (p.accumulate)
+        v += p.y[at];
+      if (p.y != nullptr)
+        p.y[at] = v;
+      if (p.y_act != nullptr)
+        p.y_act[at] = Snake(v, p.alpha_out[co]);
     }
   }
 }
@@ -140,8 +178,9 @@ __global__ __launch_bounds__(kThreads) void OutputConvKernel(OutputConvParams p)
         v[c] = p.x[static_cast<size_t>(min(c0 + c, p.cin - 1)) * p.length + tc];
 #pragma unroll
       for (int c = 0; c < kOutChunk; ++c)
-        xs[c][j] = inside && c0 + c < p.cin ? Snake(v[c], p.alpha[min(c0 + c, p.cin - 1)])
-                                            : 0.0F;
+        xs[c][j] = inside && c0 + c < p.cin
+                       ? (p.alpha != nullptr ? Snake(v[c], p.alpha[min(c0 + c, p.cin - 1)]) : v[c])
+                       : 0.0F;
     }
     __syncthreads();
     const int channels = min(kOutChunk, p.cin - c0);
@@ -170,16 +209,19 @@ __global__ __launch_bounds__(kThreads) void RvqKernel(RvqParams p) {
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WAVES>
 void DispatchConv(const ConvParams& p, hipStream_t stream) {
   const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM, p.phases);
-  Dispatch(ConvKernel<BM, BN>, grid, dim3(kThreads), 0, stream, true, true, p);
+  Dispatch(ConvKernel<BM, BN, WAVES>, grid, dim3(64 * WAVES), 0, stream, true, true, p);
 }
 
 }  // namespace
 
 void LaunchConv(const ConvParams& p, hipStream_t stream) {
-  Require(p.x && p.w && p.bias && p.y, "conv: null pointer");
+  Require(p.x && p.w && p.bias, "conv: null pointer");
+  Require(p.y != nullptr || p.y_act != nullptr, "conv: no output");
+  Require(!p.accumulate || p.y != nullptr, "conv: accumulation needs y");
+  Require(p.y_act == nullptr || p.alpha_out != nullptr, "conv: activated output needs alpha");
   Require(p.cin >= 1 && p.cout >= 1 && p.len_in >= 1 && p.positions >= 1,
           "conv: empty shape");
   Require(p.taps >= 1 && p.taps <= kConvMaxTaps, "conv: 1 to 7 taps");
@@ -195,14 +237,22 @@ void LaunchConv(const ConvParams& p, hipStream_t stream) {
     }
     Require(hi - lo <= kConvMaxSpan, "conv: taps spread over more than 64 samples");
   }
-  if (p.cout <= 32)
-    DispatchConv<32, 128>(p, stream);
+  // Four-wave tiles when they give at least one work-group per CU, else
+  // one-wave 32 x 32 tiles (four times the work-groups).
+  const auto groups = [&](int bm, int bn) {
+    return static_cast<int64_t>((p.positions + bn - 1) / bn) * ((p.cout + bm - 1) / bm) *
+           p.phases;
+  };
+  if (p.cout <= 32 && groups(32, 128) >= 256)
+    DispatchConv<32, 128, 4>(p, stream);
+  else if (p.cout > 32 && groups(64, 64) >= 256)
+    DispatchConv<64, 64, 4>(p, stream);
   else
-    DispatchConv<64, 64>(p, stream);
+    DispatchConv<32, 32, 1>(p, stream);
 }
 
 void LaunchOutputConv(const OutputConvParams& p, hipStream_t stream) {
-  Require(p.x && p.alpha && p.w && p.bias && p.y, "output conv: null pointer");
+  Require(p.x && p.w && p.bias && p.y, "output conv: null pointer");
   Require(p.cin >= 1 && p.length >= 1, "output conv: empty shape");
   Require(p.taps >= 1 && p.taps <= kConvMaxTaps && p.taps % 2 == 1,
           "output conv: 1, 3, 5 or 7 taps");

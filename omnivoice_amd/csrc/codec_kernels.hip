@@ -31,17 +31,44 @@ __device__ __forceinline__ float Snake(float v, float a) {
   return v + (1.0F / (a + 1e-9F)) * (s * s);
 }
 
-template <int BM, int BN, int WAVES>
+// Channels staged per K chunk, by tap count: every chunk feeds
+// TAPS x CHUNK / 2 MFMAs per wave between two barriers.
+template <int TAPS>
+constexpr int ChunkFor() {
+  return TAPS == 1 ? 64 : TAPS == 2 ? 32 : 16;
+}
+// Largest spread of the taps' offsets the input window allows.
+template <int TAPS>
+constexpr int SpanFor() {
+  return TAPS == 1 ? 0 : TAPS == 2 ? 1 : kConvMaxSpan;
+}
+constexpr int Pow2AtLeast(int n) {
+  int p = 1;
+  while (p < n)
+    p *= 2;
+  return p;
+}
+
+template <int BM, int BN, int WAVES, int TAPS>
 __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   static_assert(BM * BN == WAVES * 32 * 32, "one 32 x 32 block per wave");
   constexpr int kT = 64 * WAVES;
+  constexpr int kC = ChunkFor<TAPS>();
   constexpr int kWavesN = BN / 32;
-  constexpr int kWidth = BN + kConvMaxSpan;
-  constexpr int kXSlots = (kWidth + kT - 1) / kT;           // input columns per thread
-  constexpr int kWSlots = kConvMaxTaps * kChunk * BM / kT;  // weights per thread
-  static_assert(kConvMaxTaps * kChunk * BM % kT == 0, "weight slots");
-  __shared__ float xs[kChunk][kWidth];
-  __shared__ float ws[kConvMaxTaps][kChunk][BM];
+  constexpr int kWidth = BN + SpanFor<TAPS>();
+  // Staging map: thread -> column j = tid % kCols (+ kCols per extra column
+  // slot) and channels g, g + kGroups, ... with g = tid / kCols.
+  constexpr int kCols = Pow2AtLeast(kWidth) < kT ? Pow2AtLeast(kWidth) : kT;
+  constexpr int kColSlots = (kWidth + kCols - 1) / kCols;
+  constexpr int kGroups = kT / kCols;
+  constexpr int kPerGroup = kC / kGroups;  // channels per thread and column
+  static_assert(kC % kGroups == 0, "staging map");
+  constexpr int kWSlots = TAPS * kC * BM / kT;  // weights per thread
+  static_assert(TAPS * kC * BM % kT == 0, "weight slots");
+  constexpr int kSubs = kC / 16;        // 16-channel groups per tap
+  constexpr int kSteps = TAPS * kSubs;  // groups of 8 MFMAs per chunk
+  __shared__ float xs[kC][kWidth];
+  __shared__ float ws[TAPS][kC][BM];
 
   const int phase = blockIdx.z;
   const int m0 = blockIdx.x * BN;
@@ -53,52 +80,58 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   const int col = (wave % kWavesN) * 32;  // first position of the wave
   const int half = lane >> 5;             // K index of the lane's operands
   const int l32 = lane & 31;
-  const int taps = p.taps;
-  const int* offsets = p.offsets[phase];
-  int lo = offsets[0], hi = offsets[0];
-  for (int k = 1; k < taps; ++k) {
-    lo = min(lo, offsets[k]);
-    hi = max(hi, offsets[k]);
+  int shift[TAPS];
+  int lo = p.offsets[phase][0];
+#pragma unroll
+  for (int k = 0; k < TAPS; ++k) {
+    shift[k] = p.offsets[phase][k];
+    lo = min(lo, shift[k]);
   }
-  const int width = BN + hi - lo;  // <= kWidth (checked by the launcher)
-  const int weights = taps * kChunk * BM;
-  const float* w = p.w + static_cast<size_t>(phase) * taps * p.cin * p.cout;
+#pragma unroll
+  for (int k = 0; k < TAPS; ++k)
+    shift[k] -= lo;  // window column of position 0 for tap k (<= kWidth - BN)
+  const float* w = p.w + static_cast<size_t>(phase) * TAPS * p.cin * p.cout;
+  const int jcol = tid % kCols;
+  const int group = tid / kCols;
 
   // A chunk's operands pass through registers: fetch() issues the global
   // loads of chunk c0 (unconditional, clamped addresses), stash() writes
   // them to LDS with the input activation and the zero padding applied.
   // The next chunk is fetched before the current chunk's MFMAs, so its
   // loads are in flight while they run.
-  float xr[kXSlots][kChunk];
+  float xr[kColSlots][kPerGroup];
   float wr[kWSlots];
   auto fetch = [&](int c0) {
 #pragma unroll
-    for (int q = 0; q < kXSlots; ++q) {
-      const int t = min(max(m0 + lo + tid + q * kT, 0), p.len_in - 1);
+    for (int q = 0; q < kColSlots; ++q) {
+      const int t = min(max(m0 + lo + jcol + q * kCols, 0), p.len_in - 1);
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c)
-        xr[q][c] = p.x[static_cast<size_t>(min(c0 + c, p.cin - 1)) * p.len_in + t];
+      for (int i = 0; i < kPerGroup; ++i) {
+        const int c = min(c0 + group + i * kGroups, p.cin - 1);
+        xr[q][i] = p.x[static_cast<size_t>(c) * p.len_in + t];
+      }
     }
 #pragma unroll
     for (int q = 0; q < kWSlots; ++q) {
-      const int i = tid + q * kT;
-      const int o = i % BM;
-      const int c = (i / BM) % kChunk;
-      const int k = min(i / (BM * kChunk), taps - 1);
+      const int e = tid + q * kT;
+      const int o = e % BM;
+      const int c = (e / BM) % kC;
+      const int k = e / (BM * kC);
       wr[q] = w[(static_cast<size_t>(k) * p.cin + min(c0 + c, p.cin - 1)) * p.cout +
                 min(co0 + o, p.cout - 1)];
     }
   };
   auto stash = [&](int c0) {
 #pragma unroll
-    for (int q = 0; q < kXSlots; ++q) {
-      const int j = tid + q * kT;
-      if (j < width) {
+    for (int q = 0; q < kColSlots; ++q) {
+      const int j = jcol + q * kCols;
+      if (j < kWidth) {
         const int t = m0 + lo + j;
         const bool inside = t >= 0 && t < p.len_in;
 #pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-          float v = xr[q][c];
+        for (int i = 0; i < kPerGroup; ++i) {
+          const int c = group + i * kGroups;
+          float v = xr[q][i];
           if (p.alpha_in != nullptr)
             v = Snake(v, p.alpha_in[min(c0 + c, p.cin - 1)]);
           xs[c][j] = inside && c0 + c < p.cin ? v : 0.0F;
@@ -107,33 +140,53 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
     }
 #pragma unroll
     for (int q = 0; q < kWSlots; ++q) {
-      const int i = tid + q * kT;
-      if (i < weights) {
-        const int o = i % BM;
-        const int c = (i / BM) % kChunk;
-        const int k = i / (BM * kChunk);
-        ws[k][c][o] = c0 + c < p.cin && co0 + o < p.cout ? wr[q] : 0.0F;
-      }
+      const int e = tid + q * kT;
+      const int o = e % BM;
+      const int c = (e / BM) % kC;
+      const int k = e / (BM * kC);
+      ws[k][c][o] = c0 + c < p.cin && co0 + o < p.cout ? wr[q] : 0.0F;
     }
   };
 
-  // Two accumulator chains (alternate channel pairs), so that consecutive
-  // MFMAs of a wave do not wait for each other.
+  // Operands of one group of 8 MFMAs (16 channels of one tap). Groups are
+  // double-buffered in registers: group g + 1's LDS reads are issued before
+  // group g's MFMAs. Two accumulator chains (alternate channel pairs).
+  struct Operands {
+    float a[8], b[8];
+  };
+  auto read = [&](int g) {
+    const int k = g / kSubs;
+    const int c = (g % kSubs) * 16;
+    Operands op;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      op.a[s] = ws[k][c + 2 * s + half][row + l32];
+      op.b[s] = xs[c + 2 * s + half][col + l32 + shift[k]];
+    }
+    return op;
+  };
   floatx16 acc[2] = {};
   fetch(0);
-  for (int c0 = 0; c0 < p.cin; c0 += kChunk) {
+  for (int c0 = 0; c0 < p.cin; c0 += kC) {
     stash(c0);
     __syncthreads();
-    if (c0 + kChunk < p.cin)
-      fetch(c0 + kChunk);
-    for (int k = 0; k < taps; ++k) {
-      const int shift = offsets[k] - lo;
+    if (c0 + kC < p.cin)
+      fetch(c0 + kC);
+    Operands cur = read(0);
 #pragma unroll
-      for (int s = 0; s < kChunk / 2; ++s) {
-        const float a = ws[k][2 * s + half][row + l32];
-        const float b = xs[2 * s + half][col + l32 + shift];
-        acc[s & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[s & 1], 0, 0, 0);
-      }
+    for (int g = 0; g < kSteps; ++g) {
+      Operands next;
+      if (g + 1 < kSteps)
+        next = read(g + 1);
+      // Keeps the scheduler from sinking the next group's reads down to
+      // their uses, where every MFMA would wait for its own operands.
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        acc[s & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[s], cur.b[s], acc[s & 1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (g + 1 < kSteps)
+        cur = next;
     }
     __syncthreads();
   }
@@ -209,10 +262,26 @@ __global__ __launch_bounds__(kThreads) void RvqKernel(RvqParams p) {
   }
 }
 
-template <int BM, int BN, int WAVES>
+template <int BM, int BN, int WAVES, int TAPS>
 void DispatchConv(const ConvParams& p, hipStream_t stream) {
   const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM, p.phases);
-  Dispatch(ConvKernel<BM, BN, WAVES>, grid, dim3(64 * WAVES), 0, stream, true, true, p);
+  Dispatch(ConvKernel<BM, BN, WAVES, TAPS>, grid, dim3(64 * WAVES), 0, stream, true, true, p);
+}
+
+// Four-wave tiles when they give at least one work-group per CU, else
+// one-wave 32 x 32 tiles (four times the work-groups).
+template <int TAPS>
+void DispatchTaps(const ConvParams& p, hipStream_t stream) {
+  const auto groups = [&](int bm, int bn) {
+    return static_cast<int64_t>((p.positions + bn - 1) / bn) * ((p.cout + bm - 1) / bm) *
+           p.phases;
+  };
+  if (p.cout <= 32 && groups(32, 128) >= 256)
+    DispatchConv<32, 128, 4, TAPS>(p, stream);
+  else if (p.cout > 32 && groups(64, 64) >= 256)
+    DispatchConv<64, 64, 4, TAPS>(p, stream);
+  else
+    DispatchConv<32, 32, 1, TAPS>(p, stream);
 }
 
 }  // namespace
@@ -224,7 +293,7 @@ void LaunchConv(const ConvParams& p, hipStream_t stream) {
   Require(p.y_act == nullptr || p.alpha_out != nullptr, "conv: activated output needs alpha");
   Require(p.cin >= 1 && p.cout >= 1 && p.len_in >= 1 && p.positions >= 1,
           "conv: empty shape");
-  Require(p.taps >= 1 && p.taps <= kConvMaxTaps, "conv: 1 to 7 taps");
+  Require(p.taps == 1 || p.taps == 2 || p.taps == 7, "conv: 1, 2 or 7 taps");
   Require(p.phases >= 1 && p.phases <= kConvMaxPhases, "conv: 1 to 8 phases");
   Require(p.out_stride >= p.phases, "conv: phases overlap in the output");
   Require(static_cast<int64_t>(p.positions - 1) * p.out_stride + p.phases - 1 < p.len_out,
@@ -235,20 +304,16 @@ void LaunchConv(const ConvParams& p, hipStream_t stream) {
       lo = std::min(lo, p.offsets[ph][k]);
       hi = std::max(hi, p.offsets[ph][k]);
     }
-    Require(hi - lo <= kConvMaxSpan, "conv: taps spread over more than 64 samples");
+    Require(hi - lo <= (p.taps == 1 ? 0 : p.taps == 2 ? 1 : kConvMaxSpan),
+            "conv: taps spread too far for their count");
   }
-  // Four-wave tiles when they give at least one work-group per CU, else
-  // one-wave 32 x 32 tiles (four times the work-groups).
-  const auto groups = [&](int bm, int bn) {
-    return static_cast<int64_t>((p.positions + bn - 1) / bn) * ((p.cout + bm - 1) / bm) *
-           p.phases;
-  };
-  if (p.cout <= 32 && groups(32, 128) >= 256)
-    DispatchConv<32, 128, 4>(p, stream);
-  else if (p.cout > 32 && groups(64, 64) >= 256)
-    DispatchConv<64, 64, 4>(p, stream);
-  else
-    DispatchConv<32, 32, 1>(p, stream);
+  if (p.taps == 1) {
+    DispatchTaps<1>(p, stream);
+  } else if (p.taps == 2) {
+    DispatchTaps<2>(p, stream);
+  } else {
+    DispatchTaps<7>(p, stream);
+  }
 }
 
 void LaunchOutputConv(const OutputConvParams& p, hipStream_t stream) {

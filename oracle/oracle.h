@@ -22,8 +22,11 @@
  *   orc_conv1d, orc_conv_transpose1d, orc_snake
  *                        - torch.nn.functional.conv1d / conv_transpose1d
  *                          in float64 on the CPU, and the Snake closed form.
- *   orc_codec_decode     - the same composition of torch float64 layers at
- *                          a small configuration; the real-checkpoint decode
+ *   orc_codec_decode     - the installed transformers' DAC decoder (with
+ *                          HiggsAudioV2's output padding, no tanh) at a small
+ *                          configuration (tests/golden/codec_tiny.json), and
+ *                          the same composition of torch float64 layers;
+ *                          the real-checkpoint decode
  *                          vectors of the reference fixture need the codec
  *                          weights, which are absent (parity unpinned there).
  */

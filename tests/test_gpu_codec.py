@@ -100,6 +100,19 @@ def test_tiny_decode_matches_oracle(frames):
     close(got, want, rtol=2e-4)
 
 
+def test_decode_matches_transformers_fixture():
+    """The GPU decoder against transformers' DAC decoder (HiggsAudioV2's
+    output padding, no tanh) on the same synthetic weights
+    (tests/golden/codec_tiny.json)."""
+    import json
+    from conftest import GOLDEN
+    with open(os.path.join(GOLDEN, "codec_tiny.json")) as f:
+        golden = json.load(f)
+    codec = ov.Codec.synthetic(golden["config"], golden["seed"])
+    got = codec.decode(np.array(golden["codes"], dtype=np.int32))
+    close(got, np.array(golden["audio"]), rtol=2e-4)
+
+
 @pytest.fixture(scope="module")
 def released():
     cfg = ov.codec_released_config()

@@ -121,3 +121,18 @@ def test_codec_decode_matches_torch_composition(frames):
     want = _torch_decoder(TINY, 77, codes)
     assert got.shape == want.shape == (frames * 24,)
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+def test_codec_decode_matches_transformers_fixture():
+    """tests/golden/codec_tiny.json: the installed transformers' DAC decoder
+    with HiggsAudioV2's output padding and no tanh, after the RVQ decode and
+    fc2, on the synthetic weights (made by tests/golden/make_codec_golden.py)."""
+    import json
+    import os
+    from conftest import GOLDEN
+    with open(os.path.join(GOLDEN, "codec_tiny.json")) as f:
+        golden = json.load(f)
+    codes = np.array(golden["codes"], dtype=np.int32)
+    got = oracle.Codec(golden["config"], golden["seed"]).decode(codes)
+    want = np.array(golden["audio"])
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-6)

@@ -44,39 +44,42 @@
 namespace ovg {
 namespace {
 
-constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kXcds = 8;
 constexpr int kCus = 256;  // MI355X: 8 XCDs x 32 CUs
-constexpr int kABytes = kBM * kBK * 2;  // one stage of A: 16 KB
-constexpr int kBBytes = kBN * kBK * 2;
-constexpr int kStageBytes = kABytes + kBBytes;
-constexpr int kTileFloats = kBM * kBN;
+constexpr int kBBytes = kBN * kBK * 2;  // one stage of B: 16 KB
 
-// FM = 32-row MFMA blocks per wave strip: 8 waves of 32 x 128 strips (FM 1)
-// or 4 waves of 64 x 128 strips (FM 2, a quarter less LDS read traffic per
-// MFMA). Both split each K step between two groups of waves.
+// FM = 32-row MFMA blocks per wave strip. Eight waves in two K groups of
+// four strips: 128 x 128 tiles of 32-row strips (FM 1), or 256 x 128 tiles
+// of 64-row strips (FM 2: a wave's A fragment serves twice the MFMAs, so
+// the tile needs 36 % less LDS traffic and 25 % less fill per MFMA; for
+// row counts that still give every CU a tile).
 template <int FM>
 struct Shape {
-  static constexpr int kWaves = 8 / FM;
+  static constexpr int kBM = 128 * FM;
+  static constexpr int kWaves = 8;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kStrips = kWaves / 2;
   static constexpr int kOwned = 8 * FM;  // owned elements per column block
+  static constexpr int kABytes = kBM * kBK * 2;
+  static constexpr int kStageBytes = kABytes + kBBytes;
   // DMA instructions (1 KB each) per wave per stage, for A and for B.
   static constexpr int kAInstr = kABytes / 1024 / kWaves;
   static constexpr int kBInstr = kBBytes / 1024 / kWaves;
   static constexpr int kLoads = kAInstr + kBInstr;
   // The accumulator swap: every wave hands over kOwned / 4 x 4 float4 per
-  // lane (64 KB in all).
+  // lane.
   static constexpr int kSwapBytes = kThreads * kOwned * 4 * 4;
+  static constexpr int kTileFloats = kBM * kBN;
 };
 
 template <int STAGES, int FM>
 constexpr int LdsBytes() {
-  return STAGES * kStageBytes > Shape<FM>::kSwapBytes ? STAGES * kStageBytes
-                                                      : Shape<FM>::kSwapBytes;
+  using S = Shape<FM>;
+  return STAGES * S::kStageBytes > S::kSwapBytes ? STAGES * S::kStageBytes : S::kSwapBytes;
 }
+static_assert(LdsBytes<3, 2>() <= 160 * 1024, "LDS budget");
 
 // LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
 __device__ __forceinline__ uint32_t LdsAddress(const void* p) {
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
   const int tile_n = rest / p.splits;
   const int tile = tile_n * tiles_m + tile_m;
 
-  const int m0 = tile_m * kBM;
+  const int m0 = tile_m * S::kBM;
   const int n0 = tile_n * kBN;
   const int k_per = p.k / p.splits;
   const int k_begin = split * k_per;
@@ -337,7 +340,7 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
       reinterpret_cast<const unsigned char*>(p.w) + k_begin * 2;
   const uint32_t lds_base = LdsAddress(lds);
   auto issue = [&](int stage, int kt) {
-    const uint32_t base = lds_base + stage * kStageBytes;
+    const uint32_t base = lds_base + stage * S::kStageBytes;
     const int kk = kt * kBK * 2;
 #pragma unroll
     for (int i = 0; i < S::kAInstr; ++i)
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
 #pragma unroll
     for (int i = 0; i < S::kBInstr; ++i)
       DmaToLds(b_base + kk, b_src[i],
-               base + kABytes + (wave * S::kBInstr + i) * 1024);
+               base + S::kABytes + (wave * S::kBInstr + i) * 1024);
   };
 
   floatx16 acc[FM][4];
@@ -369,14 +372,14 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int rb = c * 32 + (lane & 31);
-      b_off[j][c] = kABytes + rb * 128 + Swizzle(rb, chunk) * 16;
+      b_off[j][c] = S::kABytes + rb * 128 + Swizzle(rb, chunk) * 16;
     }
   }
   struct Fragments {
     half8 a[2][FM], b[2][4];
   };
   auto read = [&](int kt) {
-    const unsigned char* s = lds + (kt % STAGES) * kStageBytes;
+    const unsigned char* s = lds + (kt % STAGES) * S::kStageBytes;
     Fragments fr;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -445,23 +448,62 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
   // the next step's LDS reads, which are issued just before them.
   // The loop body has no branch around reads: a read on only one path makes
   // the compiler wait for it on both.
-  Fragments even = read(0), odd;
-  int kt = 0;
-  for (; kt + 2 < steps; kt += 2) {
-    advance(kt);
-    odd = read(kt + 1);
-    mma(even);
-    advance(kt + 1);
-    even = read(kt + 2);
-    mma(odd);
-  }
-  if (kt + 1 < steps) {
-    advance(kt);
-    odd = read(kt + 1);
-    mma(even);
-    mma(odd);
+  if constexpr (FM == 1) {
+    Fragments even = read(0), odd;
+    int kt = 0;
+    for (; kt + 2 < steps; kt += 2) {
+      advance(kt);
+      odd = read(kt + 1);
+      mma(even);
+      advance(kt + 1);
+      even = read(kt + 2);
+      mma(odd);
+    }
+    if (kt + 1 < steps) {
+      advance(kt);
+      odd = read(kt + 1);
+      mma(even);
+      mma(odd);
+    } else {
+      mma(even);
+    }
   } else {
-    mma(even);
+    // 64-row strips hold twice the accumulators, so fragments are
+    // double-buffered per 16-wide substep instead of per K step: substep
+    // u + 1 is read while substep u's MFMAs run.
+    struct Half {
+      half8 a[FM], b[4];
+    };
+    auto read_half = [&](int kt, int j) {
+      const unsigned char* st = lds + (kt % STAGES) * S::kStageBytes;
+      Half h;
+#pragma unroll
+      for (int f = 0; f < FM; ++f)
+        h.a[f] = *reinterpret_cast<const half8*>(st + a_off[j][f]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        h.b[c] = *reinterpret_cast<const half8*>(st + b_off[j][c]);
+      return h;
+    };
+    auto mma_half = [&](const Half& h) {
+#pragma unroll
+      for (int f = 0; f < FM; ++f)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[f][c] = Mfma32(h.a[f], h.b[c], acc[f][c]);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    Half h0 = read_half(0, 0), h1;
+    for (int kt = 0; kt + 1 < steps; ++kt) {
+      h1 = read_half(kt, 1);
+      mma_half(h0);
+      advance(kt);
+      h0 = read_half(kt + 1, 0);
+      mma_half(h1);
+    }
+    h1 = read_half(steps - 1, 1);
+    mma_half(h0);
+    mma_half(h1);
   }
 
   // Swap accumulator halves. Flattening a column block's accumulators as
@@ -574,7 +616,7 @@ __global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
     for (int i = 0; i < 4; ++i)
       own.v[q / kQuads][4 * (q % kQuads) + i] = sum[q][i];
   const int tile_m = tile % tiles_m;
-  const int row0 = tile_m * kBM + 32 * FM * (wave % S::kStrips) +
+  const int row0 = tile_m * S::kBM + 32 * FM * (wave % S::kStrips) +
                    16 * FM * (wave / S::kStrips);
   OwnedEpilogue<EPI, FM>(p, own, row0, tile / tiles_m);
 }
@@ -589,34 +631,26 @@ void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
              dim3(64), 0, stream, false, true, p, tiles_m);
 }
 
-template <Epilogue EPI, int FM>
-void LaunchStages(const GemmParams& p, const GemmPlan& plan, int tiles_m,
-                  int groups, hipStream_t stream) {
-  if (plan.stages == 2)
-    Launch<2, EPI, FM>(p, tiles_m, groups, stream);
-  else if (plan.stages == 4)
-    Launch<4, EPI, FM>(p, tiles_m, groups, stream);
-  else
-    Launch<3, EPI, FM>(p, tiles_m, groups, stream);
-}
-
 template <Epilogue EPI>
 void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
-  const int tiles_m = (p.m + kBM - 1) / kBM;
   const int groups = plan.tiles * plan.splits;
-  // 32-row strips (8 waves) measured faster than 64-row strips (4 waves,
-  // one per SIMD) at every generator shape, despite the latter's lower LDS
-  // traffic per MFMA.
-  LaunchStages<EPI, 1>(p, plan, tiles_m, groups, stream);
+  if (plan.fm == 2)
+    Launch<3, EPI, 2>(p, (p.m + Shape<2>::kBM - 1) / Shape<2>::kBM, groups, stream);
+  else
+    Launch<3, EPI, 1>(p, (p.m + Shape<1>::kBM - 1) / Shape<1>::kBM, groups, stream);
 }
 
 }  // namespace
 
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   GemmPlan plan;
-  const int tiles_m = (m + kBM - 1) / kBM;
   const int tiles_n = (n + kBN - 1) / kBN;
-  plan.tiles = tiles_m * tiles_n;
+  // 256-row tiles where they still give every CU a work-group without
+  // splitting K (large M: batched chunks); 128-row tiles otherwise.
+  const int tall = (m + Shape<2>::kBM - 1) / Shape<2>::kBM * tiles_n;
+  plan.fm = epilogue != Epilogue::kPartial && tall >= kCus ? 2 : 1;
+  const int bm = plan.fm == 2 ? Shape<2>::kBM : Shape<1>::kBM;
+  plan.tiles = (m + bm - 1) / bm * tiles_n;
   plan.stages = 3;
   const int k_steps = k / kBK;
   int splits = 1;
@@ -651,8 +685,7 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   }
   plan.splits = splits;
   plan.partial_floats =
-      splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits * kTileFloats
-                 : 0;
+      splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits * bm * kBN : 0;
   return plan;
 }
 
@@ -662,8 +695,10 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
   Require(p.k % kBK == 0, "gemm: K must be a multiple of 64");
   Require(plan.splits >= 1 && (p.k / kBK) % plan.splits == 0,
           "gemm: K steps not divisible by the split count");
-  Require(plan.stages >= 2 && plan.stages <= 4, "gemm: 2 to 4 stages");
-  Require(plan.tiles == ((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN),
+  Require(plan.stages == 3, "gemm: a 3-stage ring");
+  Require(plan.fm == 1 || plan.fm == 2, "gemm: 32- or 64-row strips");
+  const int bm = plan.fm == 2 ? Shape<2>::kBM : Shape<1>::kBM;
+  Require(plan.tiles == ((p.m + bm - 1) / bm) * ((p.n + kBN - 1) / kBN),
           "gemm: plan does not match the shape");
   Require(p.lda % 8 == 0 && p.ldb % 8 == 0,
           "gemm: leading dimensions must be multiples of 8");

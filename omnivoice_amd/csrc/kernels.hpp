@@ -102,7 +102,8 @@ struct GemmParams {
 // Picks the tile shape and split count for (m, n, k) and the number of
 // floats of `partials` the launch needs.
 struct GemmPlan {
-  int stages = 3;  // LDS ring depth: 2..4
+  int stages = 3;  // LDS ring depth
+  int fm = 1;      // strip height in 32-row blocks: tiles of 128 fm rows
   int splits = 1;
   int tiles = 0;
   std::size_t partial_floats = 0;

@@ -242,6 +242,22 @@ def test_released_forward_matches_float32_oracle(released, text, target):
     assert rel_l2(got, want) < REL_L2
 
 
+def test_large_m_forward_matches_float32_oracle():
+    """Released layer dimensions (2 layers) at 1800 packed rows, where the
+    q/k/v, gate/up and head GEMMs take 256-row tiles."""
+    cfg = ov.released_config(layers=2)
+    gen = ov.Generator.synthetic(cfg, 99)
+    model = oracle.Model(cfg, 99)
+    rng = np.random.default_rng(1800)
+    ids = random_input(rng, cfg, 200, 0, 800)
+    got = gen.forward(inp(ids, 200, 800))
+    want = model.forward(ids, 200, 800)
+    print(f"max-abs {np.abs(got - want).max():.3e} rel-l2 {rel_l2(got, want):.3e}")
+    assert np.abs(got - want).max() < MAX_ABS
+    assert rel_l2(got, want) < REL_L2
+    gen.close()
+
+
 @pytest.mark.parametrize("shape", [(80, 0, 250), (180, 125, 375)])
 def test_released_generate_properties(released, shape):
     cfg, gen, _ = released

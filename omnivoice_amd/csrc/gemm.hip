@@ -645,10 +645,16 @@ void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   GemmPlan plan;
   const int tiles_n = (n + kBN - 1) / kBN;
-  // 256-row tiles where they still give every CU a work-group without
-  // splitting K (large M: batched chunks); 128-row tiles otherwise.
+  // 256-row tiles when they take fewer rounds of work-groups over the CUs,
+  // counting a 256-row tile as 1.5 128-row tiles (twice the MFMAs at a
+  // quarter less LDS traffic and fill per MFMA, the same fixed costs):
+  // large M, and shapes whose 128-row tiles spill a few work-groups into a
+  // second round (the audio heads at 500 rows: 260 tiles).
+  const int wide = (m + Shape<1>::kBM - 1) / Shape<1>::kBM * tiles_n;
   const int tall = (m + Shape<2>::kBM - 1) / Shape<2>::kBM * tiles_n;
-  plan.fm = epilogue != Epilogue::kPartial && tall >= kCus ? 2 : 1;
+  const int rounds_wide = (wide + kCus - 1) / kCus;
+  const int rounds_tall = (tall + kCus - 1) / kCus;
+  plan.fm = epilogue != Epilogue::kPartial && 3 * rounds_tall < 2 * rounds_wide ? 2 : 1;
   const int bm = plan.fm == 2 ? Shape<2>::kBM : Shape<1>::kBM;
   plan.tiles = (m + bm - 1) / bm * tiles_n;
   plan.stages = 3;

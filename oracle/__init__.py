@@ -41,6 +41,17 @@ class OrcCodecConfig(ctypes.Structure):
                 ("channels", _i64), ("blocks", _i64), ("ratios", _i64 * 8)]
 
 
+class OrcEncoderConfig(ctypes.Structure):
+    _fields_ = [("sample_rate", _i64), ("semantic_rate", _i64), ("frame_samples", _i64),
+                ("semantic_stride", _i64), ("feat_layers", _i64), ("conv_dim", _i64 * 8),
+                ("conv_kernel", _i64 * 8), ("conv_stride", _i64 * 8), ("width", _i64),
+                ("intermediate", _i64), ("heads", _i64), ("layers", _i64),
+                ("pos_kernel", _i64), ("pos_groups", _i64), ("eps", _f32),
+                ("enc_channels", _i64), ("latent", _i64), ("blocks", _i64),
+                ("ratios", _i64 * 8), ("codebooks", _i64), ("codebook_size", _i64),
+                ("codebook_dim", _i64)]
+
+
 def build(reference: bool = True) -> None:
     """Compiles liboracle.so and, when the reference tree is present,
     _ref/libref_decoding.so."""
@@ -101,6 +112,10 @@ def lib() -> ctypes.CDLL:
         "orc_codec_synthetic": (_ptr, [ctypes.POINTER(OrcCodecConfig), _u64]),
         "orc_codec_destroy": (None, [_ptr]),
         "orc_codec_decode": (_i64, [_ptr, _ptr, _i64, _ptr]),
+        "orc_resample": (_i64, [_ptr, _i64, _u32, _u32, _ptr]),
+        "orc_encoder_synthetic": (_ptr, [ctypes.POINTER(OrcEncoderConfig), _u64]),
+        "orc_encoder_destroy": (None, [_ptr]),
+        "orc_encoder_encode": (_i64, [_ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -358,5 +373,79 @@ class Codec:
     def __del__(self):
         try:
             lib().orc_codec_destroy(self._h)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ encoder
+
+def encoder_released_config() -> dict:
+    """The released audio tokenizer's encoder (tests/config_samples.hpp:34-70
+    of the reference): HuBERT base at 16 kHz (7 feature convolutions of 512
+    channels, 12 layers of 768 x 3072, 12 heads, positional convolution 128
+    taps in 16 groups), semantic stride 2, DAC encoder 64 channels doubling
+    over strides 8 5 4 2 3 to latent 256, 8 codebooks of 1024 x 64."""
+    return dict(sample_rate=24000, semantic_rate=16000, frame_samples=960, semantic_stride=2,
+                conv_dim=[512] * 7, conv_kernel=[10, 3, 3, 3, 3, 2, 2],
+                conv_stride=[5, 2, 2, 2, 2, 2, 2], width=768, intermediate=3072, heads=12,
+                layers=12, pos_kernel=128, pos_groups=16, eps=1e-5, enc_channels=64,
+                latent=256, ratios=[8, 5, 4, 2, 3], codebooks=8, codebook_size=1024,
+                codebook_dim=64)
+
+
+def encoder_tiny_config() -> dict:
+    """A small encoder of the same structure: 24 samples per frame (ratios
+    2 3 4), HuBERT strides 2 2 2 at 16 kHz (two steps per frame)."""
+    return dict(sample_rate=24000, semantic_rate=16000, frame_samples=24, semantic_stride=2,
+                conv_dim=[16, 16, 16], conv_kernel=[4, 3, 2], conv_stride=[2, 2, 2], width=32,
+                intermediate=48, heads=4, layers=2, pos_kernel=8, pos_groups=4, eps=1e-5,
+                enc_channels=4, latent=12, ratios=[2, 3, 4], codebooks=3, codebook_size=16,
+                codebook_dim=8)
+
+
+def encoder_config_struct(cfg: dict) -> OrcEncoderConfig:
+    def arr(v):
+        return (_i64 * 8)(*v)
+    return OrcEncoderConfig(cfg["sample_rate"], cfg["semantic_rate"], cfg["frame_samples"],
+                            cfg["semantic_stride"], len(cfg["conv_dim"]), arr(cfg["conv_dim"]),
+                            arr(cfg["conv_kernel"]), arr(cfg["conv_stride"]), cfg["width"],
+                            cfg["intermediate"], cfg["heads"], cfg["layers"], cfg["pos_kernel"],
+                            cfg["pos_groups"], cfg["eps"], cfg["enc_channels"], cfg["latent"],
+                            len(cfg["ratios"]), arr(cfg["ratios"]), cfg["codebooks"],
+                            cfg["codebook_size"], cfg["codebook_dim"])
+
+
+def resample(samples, from_rate: int, to_rate: int) -> np.ndarray:
+    x = np.ascontiguousarray(samples, dtype=np.float32)
+    out = np.empty(int(np.ceil(to_rate * len(x) / from_rate)) + 1, dtype=np.float32)
+    n = lib().orc_resample(_p(x), len(x), from_rate, to_rate, _p(out))
+    return out[:n]
+
+
+class Encoder:
+    """The CPU audio encoder with synthetic (seeded) weights."""
+
+    def __init__(self, cfg: dict, seed: int = 1234):
+        self.cfg = dict(cfg)
+        self._c = encoder_config_struct(cfg)
+        self._h = lib().orc_encoder_synthetic(ctypes.byref(self._c), seed)
+
+    def encode(self, samples) -> dict:
+        x = np.ascontiguousarray(samples, dtype=np.float32)
+        c = self.cfg
+        count = len(x) // c["frame_samples"]
+        hidden = c["width"] + c["latent"]
+        codes = np.zeros((c["codebooks"], count), dtype=np.int32)
+        sem = np.zeros((count, c["width"]), dtype=np.float32)
+        ac = np.zeros((count, c["latent"]), dtype=np.float32)
+        emb = np.zeros((count, hidden), dtype=np.float32)
+        n = lib().orc_encoder_encode(self._h, _p(x), len(x), _p(codes), _p(sem), _p(ac), _p(emb))
+        if n < 0:
+            raise ValueError(f"encode failed ({n})")
+        return dict(codes=codes, semantic=sem, acoustic=ac, embeddings=emb)
+
+    def __del__(self):
+        try:
+            lib().orc_encoder_destroy(self._h)
         except Exception:
             pass

@@ -150,6 +150,28 @@ void orc_codec_destroy(void* codec);
 int64_t orc_codec_decode(const void* codec, const int32_t* codes,
                          int64_t frames, float* audio);
 
+/* codec_encoder.cpp: the audio encoder (codec_encoder.cpp:249-492) */
+typedef struct orc_encoder_config {
+  int64_t sample_rate, semantic_rate, frame_samples, semantic_stride;
+  int64_t feat_layers, conv_dim[8], conv_kernel[8], conv_stride[8];
+  int64_t width, intermediate, heads, layers, pos_kernel, pos_groups;
+  float eps;
+  int64_t enc_channels, latent, blocks, ratios[8];
+  int64_t codebooks, codebook_size, codebook_dim;
+} orc_encoder_config;
+int64_t orc_resample(const float* samples, int64_t length, uint32_t from_rate,
+                     uint32_t to_rate, float* output);
+void* orc_encoder_synthetic(const orc_encoder_config* config, uint64_t seed);
+void orc_encoder_destroy(void* encoder);
+/* samples: a whole number of frames at sample_rate. codes [codebooks][count];
+ * optional stage outputs, frame-major: semantic features [count][width],
+ * acoustic [count][latent], embeddings (after fc) [count][width + latent].
+ * Returns count, or < 0 (-1 not whole frames, -2 too short for the semantic
+ * stride, -3 acoustic and semantic frame counts differ). */
+int64_t orc_encoder_encode(const void* encoder, const float* samples, int64_t length,
+                           int32_t* codes, float* semantic_out, float* acoustic_out,
+                           float* embeddings_out);
+
 #ifdef __cplusplus
 }
 #endif

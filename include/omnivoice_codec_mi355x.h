@@ -101,6 +101,79 @@ int ovc_op_conv_transpose1d(const float* x, int64_t in, int64_t length,
                             int64_t out, int64_t stride, float* y, void* stream,
                             char* error, size_t error_len);
 
+/* ------------------------------------------------------------ the encoder */
+
+/* The encoder's dimensions: CodecConfig's frame_samples and
+ * semantic_stride, SemanticEncoderConfig (HuBERT) and AcousticConfig's
+ * encoder half (config.hpp:28-72). The released tokenizer: sample_rate
+ * 24000, semantic_rate 16000, frame_samples 960, semantic_stride 2; 7
+ * feature convolutions of 512 channels, kernels 10 3 3 3 3 2 2, strides
+ * 5 2 2 2 2 2 2; width 768, intermediate 3072, 12 heads, 12 layers,
+ * positional convolution of 128 taps in 16 groups, eps 1e-5; enc_channels
+ * 64, latent 256, ratios 8 5 4 2 3; 8 codebooks of 1024 x 64. */
+typedef struct ovc_encoder_config {
+  int64_t sample_rate;     /* input audio, Hz */
+  int64_t semantic_rate;   /* HuBERT input, Hz */
+  int64_t frame_samples;   /* input samples per codec frame */
+  int64_t semantic_stride; /* HuBERT frames per codec frame */
+  int64_t feature_layers;  /* HuBERT feature convolutions, <= 8 */
+  int64_t conv_dim[8];
+  int64_t conv_kernel[8];
+  int64_t conv_stride[8];
+  int64_t width;           /* HuBERT hidden size */
+  int64_t intermediate;
+  int64_t heads;
+  int64_t layers;
+  int64_t pos_kernel;      /* positional convolution taps */
+  int64_t pos_groups;
+  double eps;              /* LayerNorm epsilon */
+  int64_t enc_channels;    /* DAC encoder input channels, doubled per block */
+  int64_t latent;          /* DAC encoder output channels */
+  int64_t blocks;          /* DAC downsampling blocks, <= 8 */
+  int64_t ratios[8];
+  int64_t codebooks;
+  int64_t codebook_size;
+  int64_t codebook_dim;
+} ovc_encoder_config;
+
+typedef struct ovc_encoder ovc_encoder;
+
+/* Loads the encoder half of model_root/audio_tokenizer/model.safetensors
+ * (float32 tensors under the reference's names, codec_encoder.cpp:74-240),
+ * or, when model_root is NULL or empty, the seeded synthetic encoder of
+ * `weight_seed`. Errors carry the prefix "OmniVoice audio tokenizer: ".
+ * Replaces LoadEncoder (codec_encoder.cpp:74-240). */
+int ovc_encoder_create(const ovc_encoder_config* config, const char* model_root,
+                       uint64_t weight_seed, ovc_encoder** handle, char* error,
+                       size_t error_len);
+void ovc_encoder_destroy(ovc_encoder* handle);
+
+/* Codec frames that `samples` input samples encode to. */
+int64_t ovc_encoder_frames(const ovc_encoder* handle, int64_t samples);
+
+/* 24 kHz mono samples (host, a whole number of frames) to codes
+ * [codebooks][frames] (host). semantic [frames][width] (the averaged HuBERT
+ * features), acoustic [frames][latent] (the DAC encoder output) and
+ * embeddings [frames][codebooks' hidden] (fc's output, the quantizer's
+ * input) are optional host outputs (NULL to skip). Errors carry the prefix
+ * "OmniVoice encode: ". Replaces Codec::Encode (codec_encoder.cpp:249-492). */
+int ovc_encode(ovc_encoder* handle, const float* samples, int64_t length,
+               int32_t* codes, float* semantic, float* acoustic,
+               float* embeddings, char* error, size_t error_len);
+
+/* ovc_encode on device buffers, enqueued on `stream` (hipStream_t, NULL =
+ * the default stream); does not synchronise. */
+int ovc_encode_device(ovc_encoder* handle, const float* samples, int64_t length,
+                      int32_t* codes, void* stream, char* error,
+                      size_t error_len);
+
+/* Per-kernel timings of `repeats` encodes of `length` samples of a
+ * synthetic signal (HIP events around every launch), as
+ * ovc_profile_decode. */
+int ovc_profile_encode(ovc_encoder* handle, int64_t length, int64_t repeats,
+                       ovg_kernel_stat* stats, int64_t capacity, int64_t* count,
+                       char* error, size_t error_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,17 @@ class _CodecConfig(ctypes.Structure):
                 ("blocks", _i64), ("ratios", _i64 * 8)]
 
 
+class _EncoderConfig(ctypes.Structure):
+    _fields_ = [("sample_rate", _i64), ("semantic_rate", _i64), ("frame_samples", _i64),
+                ("semantic_stride", _i64), ("feature_layers", _i64), ("conv_dim", _i64 * 8),
+                ("conv_kernel", _i64 * 8), ("conv_stride", _i64 * 8), ("width", _i64),
+                ("intermediate", _i64), ("heads", _i64), ("layers", _i64),
+                ("pos_kernel", _i64), ("pos_groups", _i64), ("eps", ctypes.c_double),
+                ("enc_channels", _i64), ("latent", _i64), ("blocks", _i64),
+                ("ratios", _i64 * 8), ("codebooks", _i64), ("codebook_size", _i64),
+                ("codebook_dim", _i64)]
+
+
 _CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
 
 EXPORTS = {
@@ -133,6 +144,15 @@ EXPORTS = {
                                      ctypes.c_int, _ptr, _ptr, _err, _sz]),
     "ovc_op_conv_transpose1d": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64,
                                                _i64, _ptr, _ptr, _err, _sz]),
+    # the audio encoder (include/omnivoice_codec_mi355x.h)
+    "ovc_encoder_create": (ctypes.c_int, [ctypes.POINTER(_EncoderConfig), ctypes.c_char_p,
+                                          _u64, ctypes.POINTER(_ptr), _err, _sz]),
+    "ovc_encoder_destroy": (None, [_ptr]),
+    "ovc_encoder_frames": (_i64, [_ptr, _i64]),
+    "ovc_encode": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _err, _sz]),
+    "ovc_encode_device": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _ptr, _err, _sz]),
+    "ovc_profile_encode": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _i64,
+                                          ctypes.POINTER(_i64), _err, _sz]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -618,3 +638,117 @@ def op_conv_transpose1d(x, w, b, y, stride: int, alpha=None, stream=None) -> Non
                                          _dev(alpha) if alpha is not None else None,
                                          _p(w), _p(b), out, stride, _dev(y),
                                          _stream(stream), err, len(err)), err)
+
+
+# --------------------------------------------------------------- audio encoder
+
+def encoder_released_config() -> dict:
+    """The released audio tokenizer's encoder (tests/config_samples.hpp:34-70
+    of the reference): HuBERT base at 16 kHz (7 feature convolutions of 512
+    channels, 12 layers of 768 x 3072, 12 heads, positional convolution of
+    128 taps in 16 groups), semantic stride 2, the DAC encoder from 64
+    channels doubling over strides 8 5 4 2 3 to 256 latent channels, 8
+    codebooks of 1024 x 64."""
+    return dict(sample_rate=24000, semantic_rate=16000, frame_samples=960, semantic_stride=2,
+                conv_dim=[512] * 7, conv_kernel=[10, 3, 3, 3, 3, 2, 2],
+                conv_stride=[5, 2, 2, 2, 2, 2, 2], width=768, intermediate=3072, heads=12,
+                layers=12, pos_kernel=128, pos_groups=16, eps=1e-5, enc_channels=64,
+                latent=256, ratios=[8, 5, 4, 2, 3], codebooks=8, codebook_size=1024,
+                codebook_dim=64)
+
+
+def _encoder_config(cfg: dict) -> _EncoderConfig:
+    def arr(v):
+        return (_i64 * 8)(*v)
+    return _EncoderConfig(cfg["sample_rate"], cfg["semantic_rate"], cfg["frame_samples"],
+                          cfg["semantic_stride"], len(cfg["conv_dim"]), arr(cfg["conv_dim"]),
+                          arr(cfg["conv_kernel"]), arr(cfg["conv_stride"]), cfg["width"],
+                          cfg["intermediate"], cfg["heads"], cfg["layers"], cfg["pos_kernel"],
+                          cfg["pos_groups"], cfg["eps"], cfg["enc_channels"], cfg["latent"],
+                          len(cfg["ratios"]), arr(cfg["ratios"]), cfg["codebooks"],
+                          cfg["codebook_size"], cfg["codebook_dim"])
+
+
+class Encoder:
+    """The audio tokenizer's encoder on the GPU: 24 kHz mono float32 audio, a
+    whole number of frames, to codes [codebooks][frames] (codec.hpp:16-45 of
+    the reference, Encode). Not thread-safe."""
+
+    def __init__(self, handle: int, cfg: dict):
+        self._h = handle
+        self.cfg = dict(cfg)
+
+    @classmethod
+    def load(cls, cfg: dict, model_root: Optional[str] = None,
+             seed: int = 1234) -> "Encoder":
+        """model_root/audio_tokenizer/model.safetensors, or the seeded
+        synthetic encoder when model_root is None."""
+        c = _encoder_config(cfg)
+        h = _ptr()
+        err = _buf()
+        root = model_root.encode() if model_root else None
+        _check(lib().ovc_encoder_create(ctypes.byref(c), root, seed, ctypes.byref(h), err,
+                                        len(err)), err)
+        return cls(h.value, cfg)
+
+    @classmethod
+    def synthetic(cls, cfg: dict, seed: int = 1234) -> "Encoder":
+        return cls.load(cfg, None, seed)
+
+    def frames(self, samples: int) -> int:
+        return int(lib().ovc_encoder_frames(self._h, samples))
+
+    def encode(self, samples, intermediates: bool = False):
+        """Codes [codebooks][frames] (int32); with `intermediates`, a dict
+        that also holds the averaged HuBERT features [frames][width], the
+        DAC encoder output [frames][latent] and fc's output [frames][hidden]."""
+        x = np.ascontiguousarray(samples, dtype=np.float32)
+        c = self.cfg
+        n = max(self.frames(len(x)), 1)
+        codes = np.zeros((c["codebooks"], n), dtype=np.int32)
+        extra = None
+        if intermediates:
+            extra = dict(semantic=np.zeros((n, c["width"]), np.float32),
+                         acoustic=np.zeros((n, c["latent"]), np.float32),
+                         embeddings=np.zeros((n, c["width"] + c["latent"]), np.float32))
+        err = _buf()
+        _check(lib().ovc_encode(self._h, _p(x), len(x), _p(codes),
+                                _p(extra["semantic"]) if extra else None,
+                                _p(extra["acoustic"]) if extra else None,
+                                _p(extra["embeddings"]) if extra else None, err, len(err)),
+               err)
+        if extra is None:
+            return codes
+        return dict(codes=codes, **extra)
+
+    def encode_device(self, samples, codes, stream=None) -> None:
+        """samples: float32 device tensor; codes: int32 device tensor
+        [codebooks][frames]. Enqueued on `stream`."""
+        err = _buf()
+        _check(lib().ovc_encode_device(self._h, _dev(samples), samples.numel(), _dev(codes),
+                                       _stream(stream), err, len(err)), err)
+
+    def profile(self, samples: int, repeats: int = 3) -> dict:
+        cap = 64
+        stats = (_KernelStat * cap)()
+        count = _i64()
+        err = _buf()
+        _check(lib().ovc_profile_encode(self._h, samples, repeats, ctypes.cast(stats, _ptr),
+                                        cap, ctypes.byref(count), err, len(err)), err)
+        out = {}
+        for i in range(min(count.value, cap)):
+            s = stats[i]
+            out[s.name.decode()] = dict(launches=s.launches, total_ms=s.total_ms,
+                                        flops=s.flops, bytes=s.bytes)
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            lib().ovc_encoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -28,6 +28,7 @@
 #include "../../include/omnivoice_codec_mi355x.h"
 #include "checkpoint.hpp"
 #include "codec.hpp"
+#include "codec_common.hpp"
 #include "device.hpp"
 #include "host.hpp"
 #include "kernels.hpp"
@@ -54,56 +55,6 @@ constexpr int kDilations[3] = {1, 3, 9};
 //   ....res_unit(u+1).conv2.weight, .bias       + 8, + 9    0.3 / sqrt(ch), 0.01
 //   acoustic_decoder.snake1.alpha               1400        exp
 //   acoustic_decoder.conv2.weight, .bias        1401, 1402  0.1 / sqrt(7 ch), 0.01
-void SynthCodec(std::uint64_t seed, std::uint64_t id, double scale, bool exponential,
-                std::uint64_t first, std::size_t count, float* out) {
-  for (std::size_t e = 0; e < count; ++e) {
-    const double n = SynthNormal(seed, id, first + e);
-    out[e] = static_cast<float>(exponential ? std::exp(scale * n) : scale * n);
-  }
-}
-
-// A tensor source: the synthetic specification or a checkpoint.
-class Source {
- public:
-  Source(std::uint64_t seed, const SafetensorsFile* file) : seed_(seed), file_(file) {}
-  std::vector<float> Get(const std::string& name, std::initializer_list<std::int64_t> shape,
-                         std::uint64_t id, double scale, bool exponential = false) const {
-    std::size_t count = 1;
-    for (const std::int64_t d : shape)
-      count *= static_cast<std::size_t>(d);
-    std::vector<float> out(count);
-    if (file_ != nullptr) {
-      const float* data = file_->F32(name, shape);
-      std::memcpy(out.data(), data, count * sizeof(float));
-    } else {
-      SynthCodec(seed_, id, scale, exponential, 0, count, out.data());
-    }
-    return out;
-  }
-
- private:
-  std::uint64_t seed_;
-  const SafetensorsFile* file_;
-};
-
-template <typename T>
-void Upload(DeviceBuffer<T>& buffer, const std::vector<T>& host) {
-  buffer.Reserve(host.size());
-  Check(hipMemcpy(buffer.get(), host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice),
-        "upload codec weights");
-}
-
-// Conv1d weights [out][in][kernel] -> [kernel][in][out].
-std::vector<float> ConvLayout(const std::vector<float>& w, int out, int in, int kernel) {
-  std::vector<float> r(w.size());
-  for (int o = 0; o < out; ++o)
-    for (int i = 0; i < in; ++i)
-      for (int k = 0; k < kernel; ++k)
-        r[(static_cast<std::size_t>(k) * in + i) * out + o] =
-            w[(static_cast<std::size_t>(o) * in + i) * kernel + k];
-  return r;
-}
-
 // ConvTranspose1d (kernel 2s, padding ceil(s / 2)) as s phases of two taps:
 // output m s + p = sum_i w[i][o][ka] x[i][m + c] + w[i][o][ka + s] x[i][m + c - 1]
 // with ka = (p + pad) % s and c = (p + pad) / s. Tap 0 is the one at offset
@@ -481,23 +432,7 @@ struct ovc_handle {
 
 namespace {
 
-void SetError(char* error, std::size_t len, const std::string& message) {
-  if (error == nullptr || len == 0)
-    return;
-  const std::size_t n = std::min(len - 1, message.size());
-  std::memcpy(error, message.data(), n);
-  error[n] = '\0';
-}
-
-template <typename F>
-int Guard(const char* prefix, char* error, std::size_t len, F&& body) {
-  try {
-    return body();
-  } catch (const std::exception& failure) {
-    SetError(error, len, std::string(prefix) + failure.what());
-    return OVG_ERROR;
-  }
-}
+using ovg::CodecGuard;
 
 void CheckConfig(const ovc_config& c) {
   ovg::Require(c.codebooks >= 1 && c.codebook_size >= 1 && c.codebook_dim >= 1 &&
@@ -520,7 +455,7 @@ extern "C" {
 
 int ovc_create(const ovc_config* config, const char* model_root, uint64_t weight_seed,
                ovc_handle** handle, char* error, size_t error_len) {
-  return Guard("OmniVoice audio tokenizer: ", error, error_len, [&] {
+  return CodecGuard("OmniVoice audio tokenizer: ", error, error_len, [&] {
     ovg::Require(config != nullptr && handle != nullptr, "null argument");
     CheckConfig(*config);
     std::unique_ptr<ovg::SafetensorsFile> file;
@@ -542,7 +477,7 @@ int64_t ovc_samples(const ovc_handle* handle, int64_t frames) {
 
 int ovc_decode(ovc_handle* handle, const int32_t* codes, int64_t frames, float* audio,
                char* error, size_t error_len) {
-  return Guard("OmniVoice decode: ", error, error_len, [&] {
+  return CodecGuard("OmniVoice decode: ", error, error_len, [&] {
     ovg::Require(handle != nullptr, "null argument");
     handle->engine->Decode(codes, frames, audio);
     return OVG_OK;
@@ -551,7 +486,7 @@ int ovc_decode(ovc_handle* handle, const int32_t* codes, int64_t frames, float* 
 
 int ovc_decode_device(ovc_handle* handle, const int32_t* codes, int64_t frames, float* audio,
                       void* stream, char* error, size_t error_len) {
-  return Guard("OmniVoice decode: ", error, error_len, [&] {
+  return CodecGuard("OmniVoice decode: ", error, error_len, [&] {
     ovg::Require(handle != nullptr, "null argument");
     handle->engine->DecodeDevice(codes, frames, audio, static_cast<hipStream_t>(stream));
     return OVG_OK;
@@ -561,7 +496,7 @@ int ovc_decode_device(ovc_handle* handle, const int32_t* codes, int64_t frames, 
 int ovc_profile_decode(ovc_handle* handle, int64_t frames, int64_t repeats,
                        ovg_kernel_stat* stats, int64_t capacity, int64_t* count, char* error,
                        size_t error_len) {
-  return Guard("OmniVoice profile: ", error, error_len, [&] {
+  return CodecGuard("OmniVoice profile: ", error, error_len, [&] {
     ovg::Require(handle != nullptr && count != nullptr, "null argument");
     std::map<std::string, ovg::KernelStat> table;
     handle->engine->Profile(frames, repeats, &table);
@@ -595,7 +530,7 @@ int ovc_op_conv1d(const float* x, int64_t in, int64_t length, const float* alpha
                   const float* w, const float* b, int64_t out, int64_t kernel,
                   int64_t dilation, int accumulate, float* y, void* stream, char* error,
                   size_t error_len) {
-  return Guard("conv1d: ", error, error_len, [&] {
+  return CodecGuard("conv1d: ", error, error_len, [&] {
     ovg::Require(x && w && b && y, "null pointer");
     ovg::Require(in >= 1 && out >= 1 && length >= 1 && kernel >= 1 && dilation >= 1 &&
                      in * out * kernel < (int64_t{1} << 31) && length < (int64_t{1} << 31),
@@ -634,7 +569,7 @@ int ovc_op_conv1d(const float* x, int64_t in, int64_t length, const float* alpha
 int ovc_op_conv_transpose1d(const float* x, int64_t in, int64_t length, const float* alpha,
                             const float* w, const float* b, int64_t out, int64_t stride,
                             float* y, void* stream, char* error, size_t error_len) {
-  return Guard("conv_transpose1d: ", error, error_len, [&] {
+  return CodecGuard("conv_transpose1d: ", error, error_len, [&] {
     ovg::Require(x && w && b && y, "null pointer");
     ovg::Require(in >= 1 && out >= 1 && length >= 1 && stride >= 1 &&
                      stride <= ovg::kConvMaxPhases &&

@@ -30,6 +30,10 @@ __device__ __forceinline__ float Snake(float v, float a) {
   const float s = sinf(a * v);
   return v + (1.0F / (a + 1e-9F)) * (s * s);
 }
+__device__ __forceinline__ float Gelu(float v) {
+  return 0.5F * v * (1.0F + erff(v * 0.70710678118654752F));
+}
+__device__ __forceinline__ float Elu(float v) { return v > 0.0F ? v : expm1f(v); }
 
 // Channels staged per K chunk, by tap count: every chunk feeds
 // TAPS x CHUNK / 2 MFMAs per wave between two barriers.
@@ -70,7 +74,12 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   __shared__ float xs[kC][kWidth];
   __shared__ float ws[TAPS][kC][BM];
 
-  const int phase = blockIdx.z;
+  const int phase = blockIdx.z % p.phases;
+  const int batch = blockIdx.z / p.phases;
+  const float* x = p.x + batch * p.x_batch;
+  const float* bias = p.bias != nullptr ? p.bias + batch * p.b_batch : nullptr;
+  float* y = p.y != nullptr ? p.y + batch * p.y_batch : nullptr;
+  float* y_act = p.y_act != nullptr ? p.y_act + batch * p.y_batch : nullptr;
   const int m0 = blockIdx.x * BN;
   const int co0 = blockIdx.y * BM;
   const int tid = threadIdx.x;
@@ -90,7 +99,7 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
 #pragma unroll
   for (int k = 0; k < TAPS; ++k)
     shift[k] -= lo;  // window column of position 0 for tap k (<= kWidth - BN)
-  const float* w = p.w + static_cast<size_t>(phase) * TAPS * p.cin * p.cout;
+  const float* w = p.w + batch * p.w_batch + static_cast<size_t>(phase) * TAPS * p.cin * p.ldw;
   const int jcol = tid % kCols;
   const int group = tid / kCols;
 
@@ -108,7 +117,7 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
 #pragma unroll
       for (int i = 0; i < kPerGroup; ++i) {
         const int c = min(c0 + group + i * kGroups, p.cin - 1);
-        xr[q][i] = p.x[static_cast<size_t>(c) * p.len_in + t];
+        xr[q][i] = x[static_cast<size_t>(c) * p.len_in + t];
       }
     }
 #pragma unroll
@@ -117,7 +126,7 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
       const int o = e % BM;
       const int c = (e / BM) % kC;
       const int k = e / (BM * kC);
-      wr[q] = w[(static_cast<size_t>(k) * p.cin + min(c0 + c, p.cin - 1)) * p.cout +
+      wr[q] = w[(static_cast<size_t>(k) * p.cin + min(c0 + c, p.cin - 1)) * p.ldw +
                 min(co0 + o, p.cout - 1)];
     }
   };
@@ -202,13 +211,17 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
     const int co = co0 + row + 8 * (r >> 2) + 4 * half + (r & 3);
     if (co < p.cout) {
       const size_t at = static_cast<size_t>(co) * p.len_out + t;
-      float v = (acc[0][r] + acc[1][r]) + p.bias[co];
+      float v = acc[0][r] + acc[1][r];
+      if (bias != nullptr)
+        v += bias[co];
+      if (p.pre_act == kActGelu)
+        v = Gelu(v);
       if (p.accumulate)
-        v += p.y[at];
-      if (p.y != nullptr)
-        p.y[at] = v;
-      if (p.y_act != nullptr)
-        p.y_act[at] = Snake(v, p.alpha_out[co]);
+        v += y[at];
+      if (y != nullptr)
+        y[at] = v;
+      if (y_act != nullptr)
+        y_act[at] = p.out_act == kActElu ? Elu(v) : Snake(v, p.alpha_out[co]);
     }
   }
 }
@@ -264,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void RvqKernel(RvqParams p) {
 
 template <int BM, int BN, int WAVES, int TAPS>
 void DispatchConv(const ConvParams& p, hipStream_t stream) {
-  const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM, p.phases);
+  const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM, p.phases * p.batches);
   Dispatch(ConvKernel<BM, BN, WAVES, TAPS>, grid, dim3(64 * WAVES), 0, stream, true, true, p);
 }
 
@@ -274,7 +287,7 @@ template <int TAPS>
 void DispatchTaps(const ConvParams& p, hipStream_t stream) {
   const auto groups = [&](int bm, int bn) {
     return static_cast<int64_t>((p.positions + bn - 1) / bn) * ((p.cout + bm - 1) / bm) *
-           p.phases;
+           p.phases * p.batches;
   };
   if (p.cout <= 32 && groups(32, 128) >= 256)
     DispatchConv<32, 128, 4, TAPS>(p, stream);
@@ -286,11 +299,27 @@ void DispatchTaps(const ConvParams& p, hipStream_t stream) {
 
 }  // namespace
 
-void LaunchConv(const ConvParams& p, hipStream_t stream) {
-  Require(p.x && p.w && p.bias, "conv: null pointer");
+void LaunchConv(const ConvParams& params, hipStream_t stream) {
+  ConvParams p = params;
+  if (p.ldw == 0)
+    p.ldw = p.cout;
+  if (p.batches == 0)
+    p.batches = 1;
+  if (p.out_act == kActNone)
+    p.out_act = kActSnake;
+  Require(p.x && p.w, "conv: null pointer");
   Require(p.y != nullptr || p.y_act != nullptr, "conv: no output");
   Require(!p.accumulate || p.y != nullptr, "conv: accumulation needs y");
-  Require(p.y_act == nullptr || p.alpha_out != nullptr, "conv: activated output needs alpha");
+  Require(p.y_act == nullptr || p.out_act != kActSnake || p.alpha_out != nullptr,
+          "conv: activated output needs alpha");
+  Require(p.pre_act == kActNone || p.pre_act == kActGelu, "conv: bad pre-activation");
+  Require(p.out_act == kActSnake || p.out_act == kActElu, "conv: bad output activation");
+  Require(p.ldw >= p.cout, "conv: weight rows shorter than cout");
+  Require(p.batches >= 1 && static_cast<int64_t>(p.batches) * p.phases <= 65535,
+          "conv: 1 to 65535 batches x phases");
+  Require(p.batches == 1 || (p.x_batch >= 0 && p.w_batch >= 0 && p.b_batch >= 0 &&
+                             p.y_batch >= 0),
+          "conv: negative batch stride");
   Require(p.cin >= 1 && p.cout >= 1 && p.len_in >= 1 && p.positions >= 1,
           "conv: empty shape");
   Require(p.taps == 1 || p.taps == 2 || p.taps == 7, "conv: 1, 2 or 7 taps");

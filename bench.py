@@ -149,6 +149,78 @@ def bench_codec(args, torch):
     print(json.dumps(result), flush=True)
 
 
+def bench_encode(args, torch):
+    """The audio encoder on the workload's length of reference audio: samples
+    resident on the device, codes left there (Codec::Encode without the host
+    copies)."""
+    import omnivoice_amd as ov
+    cfg = ov.encoder_released_config()
+    frames = WORKLOADS[args.workload][2] * ITEMS.get(args.workload, 1)
+    length = frames * cfg["frame_samples"]
+    encoder = ov.Encoder.synthetic(cfg, 1234)
+    t = np.arange(length)
+    rng = np.random.default_rng(42)
+    host = (0.3 * np.sin(2 * np.pi * 220 * t / 24000) * (0.5 + 0.5 * np.sin(t / 900))
+            + 0.03 * rng.standard_normal(length)).astype(np.float32)
+    samples = torch.from_numpy(host).cuda()
+    codes = torch.empty((cfg["codebooks"], frames), dtype=torch.int32, device="cuda")
+    for _ in range(args.warmup):
+        encoder.encode_device(samples, codes)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        encoder.encode_device(samples, codes)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    seconds = length / 24000.0
+    stats = encoder.profile(length, repeats=args.profile_repeats)
+    kernels = {n: {"launches": s["launches"], "avg_us": s["total_ms"] / s["launches"] * 1e3,
+                   "total_ms": s["total_ms"] / args.profile_repeats,
+                   "tflops": s["flops"] / (s["total_ms"] * 1e-3) / 1e12 if s["flops"] else None}
+               for n, s in stats.items()}
+    dominant = max(stats, key=lambda n: stats[n]["total_ms"])
+    d = stats[dominant]
+    achieved = d["flops"] / (d["total_ms"] * 1e-3) / 1e12
+    total_flops = sum(s["flops"] for s in stats.values()) / args.profile_repeats
+    result = {
+        "metric": f"audio encode, {seconds:g} s of 24 kHz reference audio ({frames} frames), "
+                  f"1 GPU",
+        "value": seconds * args.steps / elapsed,
+        "unit": "audio seconds encoded per second",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded encoder weights, a modulated tone with noise)",
+        "config": {"workload": f"{args.workload}: encode of {length} samples to {frames} "
+                               f"frames x 8 codebooks",
+                   "encoder": "Higgs Audio v2 tokenizer encoder (HuBERT base at 16 kHz, "
+                              "DAC encoder 64 ch, strides 8 5 4 2 3, RVQ 8 x 1024)",
+                   "parallelism": "single GPU"},
+        "encode_rtf": (elapsed / args.steps) / seconds,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_TFLOPS, "traffic": None,
+                     "kernel": dominant,
+                     "avg_launch_us": d["total_ms"] / d["launches"] * 1e3},
+        "encode_tflops": total_flops / (elapsed / args.steps) / 1e12,
+        "kernels": kernels,
+    }
+    if args.cpu_steps > 0:
+        import oracle
+        threads = min(16, os.cpu_count() or 1)
+        oracle.lib().orc_set_threads(threads)
+        model = oracle.Encoder(oracle.encoder_released_config(), 1234)
+        sample = host[:24000]
+        t0 = time.perf_counter()
+        model.encode(sample)
+        cpu = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": 1.0 / cpu, "unit": "audio seconds encoded per second",
+                                  "cores": threads, "kind": "port",
+                                  "sample": "1 s (25 frames) encoded by the float32 oracle "
+                                            "(double sums); weight synthesis excluded"}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -160,6 +232,8 @@ def main():
     ap.add_argument("--profile-repeats", type=int, default=3)
     ap.add_argument("--codec", action="store_true",
                     help="benchmark the audio decoder on the workload's frames instead")
+    ap.add_argument("--encode", action="store_true",
+                    help="benchmark the audio encoder on the workload's length of audio")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only copy this many MiB device to device 3 times (a "
                          "copy kernel of known size for calibrating memory "
@@ -184,6 +258,9 @@ def main():
         return
     if args.codec:
         bench_codec(args, torch)
+        return
+    if args.encode:
+        bench_encode(args, torch)
         return
     import omnivoice_amd as ov
 

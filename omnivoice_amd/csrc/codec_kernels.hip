@@ -21,7 +21,6 @@ namespace ovg {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 16;     // input channels per K chunk
 constexpr int kOutTile = 256;  // samples per work-group of the output conv
 constexpr int kOutChunk = 32;  // input channels per chunk of the output conv
 
@@ -53,6 +52,22 @@ constexpr int Pow2AtLeast(int n) {
   return p;
 }
 
+// The epilogue of one output: bias, pre-activation, residual accumulation,
+// the stores.
+__device__ __forceinline__ void Finish(const ConvParams& p, const float* bias, float* y,
+                                       float* y_act, int co, size_t at, float v) {
+  if (bias != nullptr)
+    v += bias[co];
+  if (p.pre_act == kActGelu)
+    v = Gelu(v);
+  if (p.accumulate)
+    v += y[at];
+  if (y != nullptr)
+    y[at] = v;
+  if (y_act != nullptr)
+    y_act[at] = p.out_act == kActElu ? Elu(v) : Snake(v, p.alpha_out[co]);
+}
+
 template <int BM, int BN, int WAVES, int TAPS>
 __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   static_assert(BM * BN == WAVES * 32 * 32, "one 32 x 32 block per wave");
@@ -74,8 +89,12 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   __shared__ float xs[kC][kWidth];
   __shared__ float ws[TAPS][kC][BM];
 
-  const int phase = blockIdx.z % p.phases;
-  const int batch = blockIdx.z / p.phases;
+  const int split = blockIdx.z % p.splits;
+  const int rest = blockIdx.z / p.splits;  // batch x phases + phase
+  const int phase = rest % p.phases;
+  const int batch = rest / p.phases;
+  const int c_begin = split * p.split_chunks * kC;
+  const int c_end = min(p.cin, c_begin + p.split_chunks * kC);
   const float* x = p.x + batch * p.x_batch;
   const float* bias = p.bias != nullptr ? p.bias + batch * p.b_batch : nullptr;
   float* y = p.y != nullptr ? p.y + batch * p.y_batch : nullptr;
@@ -175,11 +194,11 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
     return op;
   };
   floatx16 acc[2] = {};
-  fetch(0);
-  for (int c0 = 0; c0 < p.cin; c0 += kC) {
+  fetch(c_begin);
+  for (int c0 = c_begin; c0 < c_end; c0 += kC) {
     stash(c0);
     __syncthreads();
-    if (c0 + kC < p.cin)
+    if (c0 + kC < c_end)
       fetch(c0 + kC);
     Operands cur = read(0);
 #pragma unroll
@@ -205,24 +224,47 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
   const int m = m0 + col + l32;
   if (m >= p.positions)
     return;
+  if (p.splits > 1) {
+    // partial[rest][split][co][m]
+    float* part = p.partial + (static_cast<size_t>(rest) * p.splits + split) * p.cout * p.positions;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int co = co0 + row + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (co < p.cout)
+        part[static_cast<size_t>(co) * p.positions + m] = acc[0][r] + acc[1][r];
+    }
+    return;
+  }
   const size_t t = static_cast<size_t>(m) * p.out_stride + phase;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int co = co0 + row + 8 * (r >> 2) + 4 * half + (r & 3);
-    if (co < p.cout) {
-      const size_t at = static_cast<size_t>(co) * p.len_out + t;
-      float v = acc[0][r] + acc[1][r];
-      if (bias != nullptr)
-        v += bias[co];
-      if (p.pre_act == kActGelu)
-        v = Gelu(v);
-      if (p.accumulate)
-        v += y[at];
-      if (y != nullptr)
-        y[at] = v;
-      if (y_act != nullptr)
-        y_act[at] = p.out_act == kActElu ? Elu(v) : Snake(v, p.alpha_out[co]);
-    }
+    if (co < p.cout)
+      Finish(p, bias, y, y_act, co, static_cast<size_t>(co) * p.len_out + t, acc[0][r] + acc[1][r]);
+  }
+}
+
+// Sums the split-K partials of every output in split order, then the
+// convolution's epilogue.
+__global__ __launch_bounds__(kThreads) void SplitReduceKernel(ConvParams p) {
+  const size_t per = static_cast<size_t>(p.cout) * p.positions;
+  const size_t total = per * p.batches * p.phases;
+  for (size_t e = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; e < total;
+       e += static_cast<size_t>(gridDim.x) * kThreads) {
+    const int rest = static_cast<int>(e / per);
+    const size_t within = e % per;
+    const int co = static_cast<int>(within / p.positions);
+    const int m = static_cast<int>(within % p.positions);
+    const float* part = p.partial + static_cast<size_t>(rest) * p.splits * per + within;
+    float v = 0.0F;
+    for (int s = 0; s < p.splits; ++s)
+      v += part[static_cast<size_t>(s) * per];
+    const int phase = rest % p.phases, batch = rest / p.phases;
+    const float* bias = p.bias != nullptr ? p.bias + batch * p.b_batch : nullptr;
+    float* y = p.y != nullptr ? p.y + batch * p.y_batch : nullptr;
+    float* y_act = p.y_act != nullptr ? p.y_act + batch * p.y_batch : nullptr;
+    const size_t t = static_cast<size_t>(m) * p.out_stride + phase;
+    Finish(p, bias, y, y_act, co, static_cast<size_t>(co) * p.len_out + t, v);
   }
 }
 
@@ -276,22 +318,55 @@ __global__ __launch_bounds__(kThreads) void RvqKernel(RvqParams p) {
 }
 
 template <int BM, int BN, int WAVES, int TAPS>
-void DispatchConv(const ConvParams& p, hipStream_t stream) {
-  const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM, p.phases * p.batches);
-  Dispatch(ConvKernel<BM, BN, WAVES, TAPS>, grid, dim3(64 * WAVES), 0, stream, true, true, p);
+void DispatchConv(const ConvParams& p, hipStream_t stream, bool last = true) {
+  const dim3 grid((p.positions + BN - 1) / BN, (p.cout + BM - 1) / BM,
+                  p.phases * p.batches * p.splits);
+  Dispatch(ConvKernel<BM, BN, WAVES, TAPS>, grid, dim3(64 * WAVES), 0, stream, true, last, p);
 }
 
 // Four-wave tiles when they give at least one work-group per CU, else
 // one-wave 32 x 32 tiles (four times the work-groups).
+//
+// With a split-K workspace, a one-tap convolution whose four-wave tiles
+// number under 256 instead splits its input channels (at least two chunks
+// per split) until about 512 work-groups run, and a reduction kernel
+// finishes it.
 template <int TAPS>
-void DispatchTaps(const ConvParams& p, hipStream_t stream) {
+void DispatchTaps(const ConvParams& params, hipStream_t stream) {
+  ConvParams p = params;
   const auto groups = [&](int bm, int bn) {
     return static_cast<int64_t>((p.positions + bn - 1) / bn) * ((p.cout + bm - 1) / bm) *
            p.phases * p.batches;
   };
-  if (p.cout <= 32 && groups(32, 128) >= 256)
+  constexpr int kC = ChunkFor<TAPS>();
+  const int chunks = (p.cin + kC - 1) / kC;
+  p.splits = 1;
+  p.split_chunks = chunks;
+  const bool small_m = p.cout <= 32;
+  const int64_t tiles = small_m ? groups(32, 128) : groups(64, 64);
+  if (TAPS == 1 && p.partial != nullptr && tiles < 256 && chunks >= 4) {
+    int64_t want = std::min<int64_t>((512 + tiles - 1) / tiles, chunks / 2);
+    const int64_t outputs = static_cast<int64_t>(p.cout) * p.positions * p.phases * p.batches;
+    want = std::min<int64_t>(want, p.partial_capacity / std::max<int64_t>(outputs, 1));
+    want = std::min<int64_t>(want, 65535 / (static_cast<int64_t>(p.phases) * p.batches));
+    if (want >= 2) {
+      p.split_chunks = static_cast<int>((chunks + want - 1) / want);
+      p.splits = (chunks + p.split_chunks - 1) / p.split_chunks;
+    }
+  }
+  if (p.splits > 1) {
+    if (small_m)
+      DispatchConv<32, 128, 4, TAPS>(p, stream, false);
+    else
+      DispatchConv<64, 64, 4, TAPS>(p, stream, false);
+    const size_t total = static_cast<size_t>(p.cout) * p.positions * p.phases * p.batches;
+    const int blocks = static_cast<int>(std::min<size_t>((total + kThreads - 1) / kThreads, 16384));
+    Dispatch(SplitReduceKernel, dim3(blocks), dim3(kThreads), 0, stream, false, true, p);
+    return;
+  }
+  if (small_m && tiles >= 256)
     DispatchConv<32, 128, 4, TAPS>(p, stream);
-  else if (p.cout > 32 && groups(64, 64) >= 256)
+  else if (!small_m && tiles >= 256)
     DispatchConv<64, 64, 4, TAPS>(p, stream);
   else
     DispatchConv<32, 32, 1, TAPS>(p, stream);

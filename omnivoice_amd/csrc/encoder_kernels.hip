@@ -7,11 +7,13 @@
 // twice and are bound by HBM or, at the encoder's small sizes, by launch.
 //
 // The column kernels (LayerNorm over channels, softmax over keys) read a
-// channel-major matrix along its slow dimension: a work-group owns 16
-// adjacent columns, 16 lanes of 16 threads each walk every 16th row, so
-// each row read is 64 contiguous bytes, and the partial sums meet in LDS.
+// channel-major matrix along its slow dimension: a work-group owns 8
+// adjacent columns, each column 32 lanes that hold every 32nd row in
+// registers, so each element is read once, all of a thread's loads are in
+// flight together, and the partial sums meet in LDS.
 #include <algorithm>
 #include <cfloat>
+#include <type_traits>
 
 #include "codec.hpp"
 #include "common.hpp"
@@ -22,8 +24,6 @@ namespace ovg {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kColumns = 16;  // columns per work-group of a column kernel
-constexpr int kSlices = kThreads / kColumns;
 
 __device__ __forceinline__ float Gelu(float v) {
   return 0.5F * v * (1.0F + erff(v * 0.70710678118654752F));
@@ -88,86 +88,154 @@ __global__ __launch_bounds__(kThreads) void GroupNormGeluKernel(float* x, const 
                                                                 float eps) {
   __shared__ double scratch[kThreads / 64];
   float* row = x + static_cast<size_t>(blockIdx.x) * length;
-  double s = 0.0;
-  for (int t = threadIdx.x; t < length; t += kThreads)
-    s += row[t];
-  const double mean = BlockSum(s, scratch) / length;
-  double q = 0.0;
+  // One pass for the sum and the sum of squares (double), unrolled so that
+  // eight loads are in flight per thread.
+  double s = 0.0, q = 0.0;
+#pragma unroll 8
   for (int t = threadIdx.x; t < length; t += kThreads) {
-    const double d = row[t] - mean;
-    q += d * d;
+    const double v = row[t];
+    s += v;
+    q += v * v;
   }
-  const double inv = 1.0 / sqrt(BlockSum(q, scratch) / length + eps);
+  const double mean = BlockSum(s, scratch) / length;
+  const double var = fmax(BlockSum(q, scratch) / length - mean * mean, 0.0);
+  const double inv = 1.0 / sqrt(var + eps);
   const double wc = w[blockIdx.x], bc = b[blockIdx.x];
+#pragma unroll 8
   for (int t = threadIdx.x; t < length; t += kThreads)
     row[t] = Gelu(static_cast<float>((row[t] - mean) * inv * wc + bc));
 }
 
-// Sum over the kSlices lanes of a column (threads col, col + 16, ...).
-__device__ double ColumnSum(double v, double (*scratch)[kColumns]) {
-  const int col = threadIdx.x % kColumns, slice = threadIdx.x / kColumns;
+// The column kernels: a work-group of kCols adjacent columns x kLanes lanes;
+// lane l of a column holds rows l, l + kLanes, ... (up to kPer of them) in
+// registers, so every element is read once with all its loads in flight.
+constexpr int kCols = 8;
+constexpr int kLanes = kThreads / kCols;
+
+// Sum over the lanes of a column.
+__device__ double LaneSum(double v, double (*scratch)[kCols]) {
+  const int col = threadIdx.x % kCols, lane = threadIdx.x / kCols;
   __syncthreads();
-  scratch[slice][col] = v;
+  scratch[lane][col] = v;
   __syncthreads();
   double s = 0.0;
-  for (int i = 0; i < kSlices; ++i)
+  for (int i = 0; i < kLanes; ++i)
     s += scratch[i][col];
   return s;
 }
 
+template <int kPer>
 __global__ __launch_bounds__(kThreads) void ColumnNormKernel(ColumnNormParams p) {
-  __shared__ double scratch[kSlices][kColumns];
-  const int t = blockIdx.x * kColumns + threadIdx.x % kColumns;
-  const int slice = threadIdx.x / kColumns;
-  const bool live = t < p.positions;
+  __shared__ double scratch[kLanes][kCols];
+  const int t = blockIdx.x * kCols + threadIdx.x % kCols;
+  const int lane = threadIdx.x / kCols;
   const int tc = min(t, p.positions - 1);
-  double s = 0.0;
-  for (int c = slice; c < p.channels; c += kSlices)
-    s += p.x[static_cast<size_t>(c) * p.positions + tc];
-  const double mean = ColumnSum(s, scratch) / p.channels;
-  double q = 0.0;
-  for (int c = slice; c < p.channels; c += kSlices) {
-    const double d = p.x[static_cast<size_t>(c) * p.positions + tc] - mean;
-    q += d * d;
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = min(lane + i * kLanes, p.channels - 1);
+    v[i] = p.x[static_cast<size_t>(c) * p.positions + tc];
   }
-  const double inv = 1.0 / sqrt(ColumnSum(q, scratch) / p.channels + p.eps);
-  if (!live)
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (lane + i * kLanes < p.channels)
+      s += v[i];
+  const double mean = LaneSum(s, scratch) / p.channels;
+  double q = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (lane + i * kLanes < p.channels) {
+      const double d = v[i] - mean;
+      q += d * d;
+    }
+  const double inv = 1.0 / sqrt(LaneSum(q, scratch) / p.channels + p.eps);
+  if (t >= p.positions)
     return;
-  for (int c = slice; c < p.channels; c += kSlices) {
-    const size_t at = static_cast<size_t>(c) * p.positions + t;
-    const float v = static_cast<float>((p.x[at] - mean) * inv * p.w[c] + p.b[c]);
-    p.y[at] = v;
-    if (p.sum_mode == 1)
-      p.sum[at] = v;
-    else if (p.sum_mode == 2)
-      p.sum[at] += v;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = lane + i * kLanes;
+    if (c < p.channels) {
+      const size_t at = static_cast<size_t>(c) * p.positions + t;
+      const float o = static_cast<float>((v[i] - mean) * inv * p.w[c] + p.b[c]);
+      p.y[at] = o;
+      if (p.sum_mode == 1)
+        p.sum[at] = o;
+      else if (p.sum_mode == 2)
+        p.sum[at] += o;
+    }
   }
 }
 
-__global__ __launch_bounds__(kThreads) void ColumnSoftmaxKernel(float* x, int rows, int cols,
-                                                                float scale) {
-  __shared__ double scratch[kSlices][kColumns];
-  __shared__ float peak[kSlices][kColumns];
+// Softmax down columns longer than the registers hold: three passes over
+// the rows, eight loads in flight per lane.
+__global__ __launch_bounds__(kThreads) void ColumnSoftmaxLongKernel(float* x, int rows, int cols,
+                                                                    float scale) {
+  __shared__ double scratch[kLanes][kCols];
+  __shared__ float peak[kLanes][kCols];
   float* m = x + static_cast<size_t>(blockIdx.y) * rows * cols;
-  const int col = threadIdx.x % kColumns, slice = threadIdx.x / kColumns;
-  const int t = blockIdx.x * kColumns + col;
+  const int col = threadIdx.x % kCols, lane = threadIdx.x / kCols;
+  const int t = blockIdx.x * kCols + col;
   const int tc = min(t, cols - 1);
   float hi = -FLT_MAX;
-  for (int r = slice; r < rows; r += kSlices)
+#pragma unroll 8
+  for (int r = lane; r < rows; r += kLanes)
     hi = fmaxf(hi, m[static_cast<size_t>(r) * cols + tc]);
-  peak[slice][col] = hi;
+  peak[lane][col] = hi;
   __syncthreads();
-  for (int i = 0; i < kSlices; ++i)
+  for (int i = 0; i < kLanes; ++i)
     hi = fmaxf(hi, peak[i][col]);
   double s = 0.0;
-  for (int r = slice; r < rows; r += kSlices)
+#pragma unroll 8
+  for (int r = lane; r < rows; r += kLanes)
     s += expf((m[static_cast<size_t>(r) * cols + tc] - hi) * scale);
-  const float inv = static_cast<float>(1.0 / ColumnSum(s, scratch));
+  const float inv = static_cast<float>(1.0 / LaneSum(s, scratch));
   if (t >= cols)
     return;
-  for (int r = slice; r < rows; r += kSlices) {
+#pragma unroll 8
+  for (int r = lane; r < rows; r += kLanes) {
     const size_t at = static_cast<size_t>(r) * cols + t;
     m[at] = expf((m[at] - hi) * scale) * inv;
+  }
+}
+
+template <int kPer>
+__global__ __launch_bounds__(kThreads) void ColumnSoftmaxKernel(float* x, int rows, int cols,
+                                                                float scale) {
+  __shared__ double scratch[kLanes][kCols];
+  __shared__ float peak[kLanes][kCols];
+  float* m = x + static_cast<size_t>(blockIdx.y) * rows * cols;
+  const int col = threadIdx.x % kCols, lane = threadIdx.x / kCols;
+  const int t = blockIdx.x * kCols + col;
+  const int tc = min(t, cols - 1);
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    v[i] = m[static_cast<size_t>(min(lane + i * kLanes, rows - 1)) * cols + tc];
+  float hi = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (lane + i * kLanes < rows)
+      hi = fmaxf(hi, v[i]);
+  peak[lane][col] = hi;
+  __syncthreads();
+  for (int i = 0; i < kLanes; ++i)
+    hi = fmaxf(hi, peak[i][col]);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    v[i] = expf((v[i] - hi) * scale);
+    if (lane + i * kLanes < rows)
+      s += v[i];
+  }
+  const float inv = static_cast<float>(1.0 / LaneSum(s, scratch));
+  if (t >= cols)
+    return;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int r = lane + i * kLanes;
+    if (r < rows)
+      m[static_cast<size_t>(r) * cols + t] = v[i] * inv;
   }
 }
 
@@ -252,6 +320,21 @@ __global__ __launch_bounds__(kThreads) void NearestKernel(NearestParams p) {
     p.residual[static_cast<size_t>(h) * p.frames + f] -= row[h];
 }
 
+// Register-cached column kernels hold up to 64 rows per lane: 2048 rows.
+constexpr int kMaxColumnRows = 64 * kLanes;
+
+template <typename K>
+void ColumnDispatch(int rows, K&& launch) {
+  if (rows <= 8 * kLanes)
+    launch(std::integral_constant<int, 8>());
+  else if (rows <= 16 * kLanes)
+    launch(std::integral_constant<int, 16>());
+  else if (rows <= 32 * kLanes)
+    launch(std::integral_constant<int, 32>());
+  else
+    launch(std::integral_constant<int, 64>());
+}
+
 int Blocks(size_t work) {
   return static_cast<int>(std::min<size_t>((work + kThreads - 1) / kThreads, 256 * 64));
 }
@@ -288,17 +371,28 @@ void LaunchGroupNormGelu(float* x, const float* w, const float* b, int channels,
 void LaunchColumnNorm(const ColumnNormParams& p, hipStream_t stream) {
   Require(p.x && p.y && p.w && p.b, "layer norm: null pointer");
   Require(p.sum_mode == 0 || p.sum != nullptr, "layer norm: no sum buffer");
-  Require(p.channels >= 1 && p.positions >= 1, "layer norm: empty shape");
-  Dispatch(ColumnNormKernel, dim3((p.positions + kColumns - 1) / kColumns), dim3(kThreads), 0,
-           stream, true, true, p);
+  Require(p.channels >= 1 && p.channels <= kMaxColumnRows && p.positions >= 1,
+          "layer norm: 1 to 2048 channels");
+  ColumnDispatch(p.channels, [&](auto per) {
+    Dispatch(ColumnNormKernel<decltype(per)::value>, dim3((p.positions + kCols - 1) / kCols),
+             dim3(kThreads), 0, stream, true, true, p);
+  });
 }
 
 void LaunchColumnSoftmax(float* x, int batches, int rows, int cols, float scale,
                          hipStream_t stream) {
   Require(x != nullptr, "softmax: null pointer");
   Require(batches >= 1 && batches <= 65535 && rows >= 1 && cols >= 1, "softmax: bad shape");
-  Dispatch(ColumnSoftmaxKernel, dim3((cols + kColumns - 1) / kColumns, batches), dim3(kThreads),
-           0, stream, true, true, x, rows, cols, scale);
+  if (rows > kMaxColumnRows) {
+    Dispatch(ColumnSoftmaxLongKernel, dim3((cols + kCols - 1) / kCols, batches), dim3(kThreads),
+             0, stream, true, true, x, rows, cols, scale);
+    return;
+  }
+  ColumnDispatch(rows, [&](auto per) {
+    Dispatch(ColumnSoftmaxKernel<decltype(per)::value>,
+             dim3((cols + kCols - 1) / kCols, batches), dim3(kThreads), 0, stream, true, true, x,
+             rows, cols, scale);
+  });
 }
 
 void LaunchTranspose(const float* x, int rows, int cols, int ldx, float* y,

@@ -52,7 +52,7 @@ def compare(got, want, rtol=1e-4, codes_equal=True):
         np.testing.assert_array_equal(got["codes"], want["codes"])
 
 
-@pytest.mark.parametrize("frames", [1, 9, 40])
+@pytest.mark.parametrize("frames", [1, 9, 40, 1100])  # 1100: over 2048 HuBERT steps
 def test_tiny_encode_matches_oracle(frames):
     cfg = oracle.encoder_tiny_config()
     x = signal(frames * cfg["frame_samples"], frames)

@@ -37,6 +37,7 @@ namespace ovg {
 namespace {
 
 constexpr int kResidualKernel = 7;
+constexpr std::int64_t kPartialFloats = std::int64_t{8} << 20;  // 32 MiB
 constexpr int kDilations[3] = {1, 3, 9};
 
 // Synthetic decoder specification (tensor id, scale); element = flat index
@@ -149,6 +150,9 @@ class CodecEngine {
   // (the next convolution's input; two, so that an upsampling layer reads
   // one and writes the other) and the residual branch's activated output.
   DeviceBuffer<float> latent_, x_, xa_[2], ya_, audio_;
+  // Split-K workspace of the convolutions whose output tiles leave CUs idle
+  // (the input convolution at short lengths).
+  DeviceBuffer<float> partial_;
   DeviceBuffer<std::int32_t> codes_;
   std::int64_t reserved_ = 0;
 };
@@ -238,6 +242,7 @@ CodecEngine::CodecEngine(const ovc_config& cfg, std::uint64_t seed,
                           1401, 0.1 / std::sqrt(7.0 * channels));
   Upload(out_w_, ConvLayout(ow, 1, channels, kResidualKernel));
   Upload(out_b_, src.Get("acoustic_decoder.conv2.bias", {1}, 1402, 0.01));
+  partial_.Reserve(kPartialFloats);
   Check(hipDeviceSynchronize(), "codec upload");
 }
 
@@ -270,6 +275,8 @@ void CodecEngine::RunConv(const Conv& c, const float* x, int length, float* y, f
   p.x = x;
   p.w = c.w.get();
   p.bias = c.b.get();
+  p.partial = partial_.get();
+  p.partial_capacity = kPartialFloats;
   p.y = y;
   p.y_act = y_act;
   p.alpha_out = alpha_out;
@@ -335,6 +342,8 @@ void CodecEngine::Enqueue(const std::int32_t* codes, std::int64_t frames, float*
     p.x = xa_[cur].get();
     p.w = blk.w.get();
     p.bias = blk.b.get();
+    p.partial = partial_.get();
+    p.partial_capacity = kPartialFloats;
     p.y = x_.get();
     p.y_act = xa_[1 - cur].get();
     p.alpha_out = blk.units[0].alpha1.get();

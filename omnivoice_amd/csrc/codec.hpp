@@ -52,10 +52,9 @@ struct ConvParams {
   std::int64_t x_batch, w_batch, b_batch, y_batch;  // element strides per batch
   int offsets[kConvMaxPhases][kConvMaxTaps];
   // Optional split-K workspace (float32 elements): when the output tiles
-  // alone leave CUs idle, the launcher may split the input channels of a
-  // one-tap convolution over several work-groups, which store partial sums
-  // here; a second kernel adds them in a fixed order and applies the
-  // epilogue. Null: never split.
+  // alone leave CUs idle, the launcher may split the input channels over
+  // several work-groups, which store partial sums here; a second kernel
+  // adds them in a fixed order and applies the epilogue. Null: never split.
   float* partial;
   std::int64_t partial_capacity;
   // Set by the launcher.

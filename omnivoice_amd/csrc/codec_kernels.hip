@@ -327,10 +327,10 @@ void DispatchConv(const ConvParams& p, hipStream_t stream, bool last = true) {
 // Four-wave tiles when they give at least one work-group per CU, else
 // one-wave 32 x 32 tiles (four times the work-groups).
 //
-// With a split-K workspace, a one-tap convolution whose four-wave tiles
-// number under 256 instead splits its input channels (at least two chunks
-// per split) until about 512 work-groups run, and a reduction kernel
-// finishes it.
+// With a split-K workspace, a convolution whose four-wave tiles number
+// under 256 instead splits its input channels (at least two chunks per
+// split) until about 512 work-groups run, and a reduction kernel finishes
+// it.
 template <int TAPS>
 void DispatchTaps(const ConvParams& params, hipStream_t stream) {
   ConvParams p = params;
@@ -344,7 +344,7 @@ void DispatchTaps(const ConvParams& params, hipStream_t stream) {
   p.split_chunks = chunks;
   const bool small_m = p.cout <= 32;
   const int64_t tiles = small_m ? groups(32, 128) : groups(64, 64);
-  if (TAPS == 1 && p.partial != nullptr && tiles < 256 && chunks >= 4) {
+  if (p.partial != nullptr && tiles < 256 && chunks >= 4) {
     int64_t want = std::min<int64_t>((512 + tiles - 1) / tiles, chunks / 2);
     const int64_t outputs = static_cast<int64_t>(p.cout) * p.positions * p.phases * p.batches;
     want = std::min<int64_t>(want, p.partial_capacity / std::max<int64_t>(outputs, 1));

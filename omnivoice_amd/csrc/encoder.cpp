@@ -593,6 +593,8 @@ void EncoderEngine::RunConv7(const Conv7& c, const float* x, int length, float* 
   p.positions = length;
   p.out_stride = 1;
   p.accumulate = accumulate ? 1 : 0;
+  p.partial = partial_.get();
+  p.partial_capacity = kPartialFloats;
   for (int k = 0; k < 7; ++k)
     p.offsets[0][k] = (k - 3) * c.dilation;
   const double flops = 2.0 * c.out * static_cast<double>(length) * c.in * 7;

@@ -221,6 +221,49 @@ def bench_encode(args, torch):
     print(json.dumps(result), flush=True)
 
 
+def gemm_compare(args, torch):
+    """The vendor library at the backbone's GEMM shapes, as a speed
+    comparator: torch.matmul (hipBLASLt) fp16 x fp16 -> fp16, 28 distinct
+    weight matrices per shape (one per layer, so weights stream from HBM as
+    in a step) replayed in a HIP graph; per-GEMM time = graph time / 28."""
+    shapes = [("qkv", 4096, 1024), ("gate_up", 6144, 1024), ("o", 1024, 2048),
+              ("down", 1024, 3072)]
+    rows = {"C2": 120, "C3": 580, "C4": 1055, "C5": 3440}
+    out = []
+    for config, m in rows.items():
+        for name, n, k in shapes:
+            x = torch.randn(m, k, device="cuda", dtype=torch.float16)
+            ws = [torch.randn(n, k, device="cuda", dtype=torch.float16) * 0.02
+                  for _ in range(28)]
+            ys = [torch.empty(m, n, device="cuda", dtype=torch.float16) for _ in range(28)]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for l in range(28):
+                    torch.matmul(x, ws[l].t(), out=ys[l])
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for l in range(28):
+                    torch.matmul(x, ws[l].t(), out=ys[l])
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            reps = 20
+            a.record()
+            for _ in range(reps):
+                g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / (reps * 28)
+            out.append({"config": config, "gemm": name, "m": m, "n": n, "k": k,
+                        "us": us, "tflops": 2.0 * m * n * k / us / 1e6})
+            del ws, ys, g
+    print(json.dumps({"comparator": "torch.matmul (hipBLASLt), fp16 out, HIP graph of 28",
+                      "torch": torch.__version__, "rows": out}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +277,8 @@ def main():
                     help="benchmark the audio decoder on the workload's frames instead")
     ap.add_argument("--encode", action="store_true",
                     help="benchmark the audio encoder on the workload's length of audio")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="time the vendor GEMM (torch.matmul) at the backbone's shapes")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only copy this many MiB device to device 3 times (a "
                          "copy kernel of known size for calibrating memory "
@@ -261,6 +306,9 @@ def main():
         return
     if args.encode:
         bench_encode(args, torch)
+        return
+    if args.gemm_compare:
+        gemm_compare(args, torch)
         return
     import omnivoice_amd as ov
 

@@ -287,7 +287,7 @@ __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
 
 template <int STAGES, Epilogue EPI, int FM>
 __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
-    GemmParams p, int tiles_m) {
+    GemmParams p, int tiles_m, int band) {
   using S = Shape<FM>;
   extern __shared__ __align__(16) unsigned char lds[];
 
@@ -298,10 +298,30 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
   const int per = groups / kXcds;
   const int extra = groups % kXcds;
   const int logical = xcd * per + min(xcd, extra) + pid / kXcds;
-  const int tile_m = logical % tiles_m;
-  const int rest = logical / tiles_m;
-  const int split = rest % p.splits;
-  const int tile_n = rest / p.splits;
+  int tile_m, tile_n, split;
+  if (band <= 0 || band >= tiles_m || p.splits > 1) {
+    tile_m = logical % tiles_m;
+    const int rest = logical / tiles_m;
+    split = rest % p.splits;
+    tile_n = rest / p.splits;
+  } else {
+    // Bands of `band` row tiles (the last one shorter), column by column
+    // inside a band, rows fastest (no split-K here).
+    const int tiles_n = groups / tiles_m;
+    const int full = tiles_m / band;
+    const int head = full * band * tiles_n;
+    split = 0;
+    if (logical < head) {
+      const int within = logical % (band * tiles_n);
+      tile_n = within / band;
+      tile_m = logical / (band * tiles_n) * band + within % band;
+    } else {
+      const int rows = tiles_m - full * band;
+      const int within = logical - head;
+      tile_n = within / rows;
+      tile_m = full * band + within % rows;
+    }
+  }
   const int tile = tile_n * tiles_m + tile_m;
 
   const int m0 = tile_m * S::kBM;
@@ -622,10 +642,10 @@ __global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
 }
 
 template <int STAGES, Epilogue EPI, int FM>
-void Launch(const GemmParams& p, int tiles_m, int groups, hipStream_t stream) {
+void Launch(const GemmParams& p, int tiles_m, int band, int groups, hipStream_t stream) {
   const bool reduce = p.splits > 1 && EPI != Epilogue::kPartial;
   Dispatch(GemmKernel<STAGES, EPI, FM>, dim3(groups), dim3(Shape<FM>::kThreads),
-           LdsBytes<STAGES, FM>(), stream, true, !reduce, p, tiles_m);
+           LdsBytes<STAGES, FM>(), stream, true, !reduce, p, tiles_m, band);
   if (reduce)
     Dispatch(SplitReduceKernel<EPI, FM>, dim3(groups / p.splits * Shape<FM>::kWaves),
              dim3(64), 0, stream, false, true, p, tiles_m);
@@ -635,12 +655,27 @@ template <Epilogue EPI>
 void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
   const int groups = plan.tiles * plan.splits;
   if (plan.fm == 2)
-    Launch<3, EPI, 2>(p, (p.m + Shape<2>::kBM - 1) / Shape<2>::kBM, groups, stream);
+    Launch<3, EPI, 2>(p, (p.m + Shape<2>::kBM - 1) / Shape<2>::kBM, plan.band, groups, stream);
   else
-    Launch<3, EPI, 1>(p, (p.m + Shape<1>::kBM - 1) / Shape<1>::kBM, groups, stream);
+    Launch<3, EPI, 1>(p, (p.m + Shape<1>::kBM - 1) / Shape<1>::kBM, plan.band, groups, stream);
 }
 
 }  // namespace
+
+// X bytes per band of row tiles (see GemmPlan::band).
+constexpr std::int64_t kBandBytes = std::int64_t{2} << 20;
+
+// Banded tile order once all rows of X outgrow what an XCD's L2 keeps
+// beside the weight tiles: bands of at most kBandBytes of X. Split-K
+// launches keep the plain order.
+int BandFor(int m, int k, int bm, int splits) {
+  const int tiles_m = (m + bm - 1) / bm;
+  if (splits > 1)
+    return tiles_m;
+  const std::int64_t row_tile_bytes = static_cast<std::int64_t>(bm) * k * 2;
+  return static_cast<int>(std::max<std::int64_t>(
+      1, std::min<std::int64_t>(tiles_m, kBandBytes / row_tile_bytes)));
+}
 
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   GemmPlan plan;
@@ -677,6 +712,7 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
     }
     plan.splits = splits;
     plan.partial_floats = 0;
+    plan.band = BandFor(m, k, bm, splits);
     return plan;
   }
   // Otherwise split K only when the tiles leave most CUs idle; partials
@@ -692,6 +728,7 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   plan.splits = splits;
   plan.partial_floats =
       splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits * bm * kBN : 0;
+  plan.band = BandFor(m, k, bm, splits);
   return plan;
 }
 

@@ -106,6 +106,11 @@ struct GemmPlan {
   int fm = 1;      // strip height in 32-row blocks: tiles of 128 fm rows
   int splits = 1;
   int tiles = 0;
+  // Row tiles per band of the tile order: each XCD takes a run of tiles
+  // that covers `band` row tiles across columns, so its rows of X stay in
+  // its L2 (0 or all row tiles: plain M-fastest order; always so with
+  // split-K).
+  int band = 0;
   std::size_t partial_floats = 0;
 };
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue);

@@ -334,11 +334,16 @@ def main():
         run(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    # generate returns the codes on the host, so every utterance ends
+    # synchronised: its own wall time needs no extra synchronisation.
+    marks = [t0]
     for i in range(args.steps):
         run(i)
+        marks.append(time.perf_counter())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_utterance = elapsed / args.steps * 1e3
+    each_ms = sorted((b - a) * 1e3 for a, b in zip(marks, marks[1:]))
     steps_per_s = executed * items * args.steps / elapsed
     rtf = (elapsed / args.steps) / (items * target / 25.0)
 
@@ -409,6 +414,8 @@ def main():
                    "backbone": "28 x Qwen3 (hidden 1024, 16q/8kv x 128, FFN 3072)",
                    "parallelism": "single GPU"},
         "utterance_rtf": rtf,
+        "utterance_ms": {"median": each_ms[len(each_ms) // 2], "min": each_ms[0],
+                         "max": each_ms[-1]},
         "unmask_steps_per_utterance": executed,
         "roofline": roofline,
         "backbone_gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,

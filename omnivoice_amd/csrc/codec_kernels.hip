@@ -236,11 +236,32 @@ __global__ __launch_bounds__(64 * WAVES) void ConvKernel(ConvParams p) {
     return;
   }
   const size_t t = static_cast<size_t>(m) * p.out_stride + phase;
+  // Every load of the epilogue (bias, the residual, the Snake alphas) is
+  // issued before its first store: the stores may alias them as far as the
+  // compiler knows, so loads left between them would each wait out a
+  // memory round trip.
+  float b[16], prior[16], a[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int co = min(co0 + row + 8 * (r >> 2) + 4 * half + (r & 3), p.cout - 1);
+    b[r] = bias != nullptr ? bias[co] : 0.0F;
+    prior[r] = p.accumulate ? y[static_cast<size_t>(co) * p.len_out + t] : 0.0F;
+    a[r] = y_act != nullptr && p.out_act == kActSnake ? p.alpha_out[co] : 0.0F;
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int co = co0 + row + 8 * (r >> 2) + 4 * half + (r & 3);
-    if (co < p.cout)
-      Finish(p, bias, y, y_act, co, static_cast<size_t>(co) * p.len_out + t, acc[0][r] + acc[1][r]);
+    if (co < p.cout) {
+      const size_t at = static_cast<size_t>(co) * p.len_out + t;
+      float v = (acc[0][r] + acc[1][r]) + b[r];
+      if (p.pre_act == kActGelu)
+        v = Gelu(v);
+      v += prior[r];
+      if (y != nullptr)
+        y[at] = v;
+      if (y_act != nullptr)
+        y_act[at] = p.out_act == kActElu ? Elu(v) : Snake(v, a[r]);
+    }
   }
 }
 

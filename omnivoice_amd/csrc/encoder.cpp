@@ -986,6 +986,8 @@ void CheckEncoderConfig(const ovc_encoder_config& c) {
             "bad feature convolution");
   Require(c.width >= 1 && c.intermediate >= 1 && c.heads >= 1 && c.width % c.heads == 0,
           "width must split into heads");
+  Require(c.width <= 1024 && c.conv_dim[c.feature_layers - 1] <= 1024,
+          "HuBERT widths above 1024 are not supported");
   Require(c.layers >= 0 && c.layers <= 64, "0 to 64 layers");
   Require(c.pos_kernel >= 1 && c.pos_groups >= 1 && c.width % c.pos_groups == 0,
           "width must split into positional groups");

@@ -152,17 +152,27 @@ __global__ __launch_bounds__(kThreads) void ColumnNormKernel(ColumnNormParams p)
   const double inv = 1.0 / sqrt(LaneSum(q, scratch) / p.channels + p.eps);
   if (t >= p.positions)
     return;
+  // Every load of the store loop first, all in flight together: y may alias
+  // them as far as the compiler knows, so loads left inside the loop would
+  // each wait out a memory round trip behind the previous store.
+  float w[kPer], b[kPer];
+  double prior[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = min(lane + i * kLanes, p.channels - 1);
+    w[i] = p.w[c];
+    b[i] = p.b[c];
+    prior[i] = p.sum_mode == 2 ? p.sum[static_cast<size_t>(c) * p.positions + t] : 0.0;
+  }
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = lane + i * kLanes;
     if (c < p.channels) {
       const size_t at = static_cast<size_t>(c) * p.positions + t;
-      const float o = static_cast<float>((v[i] - mean) * inv * p.w[c] + p.b[c]);
+      const float o = static_cast<float>((v[i] - mean) * inv * w[i] + b[i]);
       p.y[at] = o;
-      if (p.sum_mode == 1)
-        p.sum[at] = o;
-      else if (p.sum_mode == 2)
-        p.sum[at] += o;
+      if (p.sum_mode != 0)
+        p.sum[at] = prior[i] + o;
     }
   }
 }
@@ -320,8 +330,10 @@ __global__ __launch_bounds__(kThreads) void NearestKernel(NearestParams p) {
     p.residual[static_cast<size_t>(h) * p.frames + f] -= row[h];
 }
 
-// Register-cached column kernels hold up to 64 rows per lane: 2048 rows.
+// Register-cached column kernels hold up to 64 rows per lane: 2048 rows
+// (LayerNorm, which also holds its weights and running sums: 1024).
 constexpr int kMaxColumnRows = 64 * kLanes;
+constexpr int kMaxNormChannels = 32 * kLanes;
 
 template <typename K>
 void ColumnDispatch(int rows, K&& launch) {
@@ -371,11 +383,12 @@ void LaunchGroupNormGelu(float* x, const float* w, const float* b, int channels,
 void LaunchColumnNorm(const ColumnNormParams& p, hipStream_t stream) {
   Require(p.x && p.y && p.w && p.b, "layer norm: null pointer");
   Require(p.sum_mode == 0 || p.sum != nullptr, "layer norm: no sum buffer");
-  Require(p.channels >= 1 && p.channels <= kMaxColumnRows && p.positions >= 1,
-          "layer norm: 1 to 2048 channels");
+  Require(p.channels >= 1 && p.channels <= kMaxNormChannels && p.positions >= 1,
+          "layer norm: 1 to 1024 channels");
   ColumnDispatch(p.channels, [&](auto per) {
-    Dispatch(ColumnNormKernel<decltype(per)::value>, dim3((p.positions + kCols - 1) / kCols),
-             dim3(kThreads), 0, stream, true, true, p);
+    if constexpr (decltype(per)::value <= kMaxNormChannels / kLanes)
+      Dispatch(ColumnNormKernel<decltype(per)::value>, dim3((p.positions + kCols - 1) / kCols),
+               dim3(kThreads), 0, stream, true, true, p);
   });
 }
 

@@ -285,7 +285,7 @@ def main():
                          "counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+        print(json.dumps({"error": "this library runs on one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is design-only)"}))
         sys.exit(2)
 

@@ -3,8 +3,8 @@
 ctypes bindings of the CPU restatement (liboracle.so, built by
 oracle/Makefile) and of the reference's own decoding.cpp compiled into
 oracle/_ref/. Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg import this package, as the checker or as the timed CPU
-baseline; the product package never does.
+cpu_baseline leg import this package, to check the product's results or as
+the timed CPU baseline; the product package never does.
 """
 from __future__ import annotations
 

@@ -4,8 +4,8 @@
  * A CPU restatement of the reference's unmasking generator (gufo-extensions/
  * omnivoice): decoding.cpp:12-107, generator.cpp:175-301,
  * kernels/generator_kernels.hip:62-265. Only tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg load it, and only as the checker or as the
- * timed CPU baseline. The product (omnivoice_amd/) never links or calls it.
+ * and bench.py's cpu_baseline leg load it, and only to check the product's
+ * results or as the timed CPU baseline. The product (omnivoice_amd/) never links or calls it.
  *
  * Pinning (what fixes each function, besides the GPU comparison):
  *   orc_unmask_schedule  - the reference fixture's three 32-step schedules,

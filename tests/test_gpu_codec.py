@@ -52,6 +52,9 @@ def close(got, want, rtol=1e-4):
     (21, 40, 64, 1, 1, True, True),       # ragged input channels, one tap
     (256, 1024, 25, 7, 1, False, False),  # the decoder's input convolution shape
     (64, 64, 5, 7, 9, True, False),       # signal shorter than the taps' spread
+    (128, 128, 40000, 7, 1, True, True),  # long signals: hundreds of tiles
+    (64, 64, 40000, 7, 3, True, False),
+    (48, 96, 40000, 1, 1, True, True),    # long, one tap, ragged channels
 ])
 def test_conv1d_matches_oracle(cin, cout, length, kernel, dilation, snake, accumulate):
     rng = np.random.default_rng(cin + cout + length)
@@ -70,7 +73,8 @@ def test_conv1d_matches_oracle(cin, cout, length, kernel, dilation, snake, accum
 
 @pytest.mark.parametrize("cin,cout,length,stride,snake", [
     (64, 32, 40, 8, True), (32, 16, 33, 5, True), (128, 64, 70, 4, False),
-    (16, 8, 9, 2, True), (48, 24, 31, 3, True), (1024, 512, 25, 8, True)])
+    (16, 8, 9, 2, True), (48, 24, 31, 3, True), (1024, 512, 25, 8, True),
+    (256, 128, 10000, 4, True)])  # long signal over four phases
 def test_conv_transpose1d_matches_oracle(cin, cout, length, stride, snake):
     rng = np.random.default_rng(cin * stride + length)
     x = rng.standard_normal((cin, length)).astype(np.float32)

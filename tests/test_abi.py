@@ -97,3 +97,22 @@ def test_codec_config_and_file_errors_before_the_gpu():
     with pytest.raises(ov.GeneratorError,
                        match="^OmniVoice audio tokenizer: .*audio_tokenizer/model.safetensors"):
         ov.Codec.load(cfg, "/nonexistent")
+
+
+def test_encoder_config_and_file_errors_before_the_gpu():
+    """The encoder's configuration and checkpoint errors carry the reference's
+    prefix and come before any device work (codec_encoder.cpp:74-240)."""
+    cfg = ov.encoder_released_config()
+    prefix = "^OmniVoice audio tokenizer: "
+    with pytest.raises(ov.GeneratorError, match=prefix + "ratios must multiply to frame_samples"):
+        ov.Encoder.load(dict(cfg, ratios=[8, 5, 4, 2, 2]))
+    with pytest.raises(ov.GeneratorError, match=prefix + "width must split into heads"):
+        ov.Encoder.load(dict(cfg, heads=7))
+    with pytest.raises(ov.GeneratorError, match=prefix + "width must split into positional"):
+        ov.Encoder.load(dict(cfg, pos_groups=7))
+    with pytest.raises(ov.GeneratorError, match=prefix + "HuBERT widths above 1024"):
+        ov.Encoder.load(dict(cfg, width=1536, heads=12, pos_groups=16))
+    with pytest.raises(ov.GeneratorError, match=prefix + "1 to 8 feature convolutions"):
+        ov.Encoder.load(dict(cfg, conv_dim=[], conv_kernel=[], conv_stride=[]))
+    with pytest.raises(ov.GeneratorError, match=prefix + ".*audio_tokenizer/model.safetensors"):
+        ov.Encoder.load(cfg, "/nonexistent")

@@ -155,7 +155,8 @@ def test_rmsnorm_matches_oracle():
 # ------------------------------------------------------------------ attention
 
 @pytest.mark.parametrize("seqs", [[(0, 330), (336, 250)], [(0, 1), (16, 31)],
-                                  [(0, 680), (688, 375)], [(0, 33)]])
+                                  [(0, 680), (688, 375)], [(0, 33)],
+                                  [(0, 1500), (1504, 700)]])  # 12 and 6 rounds of 4 key tiles
 def test_attention_matches_oracle(seqs):
     rng = np.random.default_rng(len(seqs) + seqs[-1][1])
     heads, kv = 16, 8

@@ -55,12 +55,15 @@ constexpr int kBBytes = kBN * kBK * 2;  // one stage of B: 16 KB
 // of 64-row strips (FM 2: a wave's A fragment serves twice the MFMAs, so
 // the tile needs 36 % less LDS traffic and 25 % less fill per MFMA; for
 // row counts that still give every CU a tile).
-template <int FM>
+//
+// STRIPS = strips per K group: four (eight waves), or one (two waves:
+// 32 x 128 tiles, for row counts whose 128-row tiles leave most CUs idle).
+template <int FM, int STRIPS = 4>
 struct Shape {
-  static constexpr int kBM = 128 * FM;
-  static constexpr int kWaves = 8;
+  static constexpr int kBM = 32 * FM * STRIPS;
+  static constexpr int kWaves = 2 * STRIPS;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kStrips = kWaves / 2;
+  static constexpr int kStrips = STRIPS;
   static constexpr int kOwned = 8 * FM;  // owned elements per column block
   static constexpr int kABytes = kBM * kBK * 2;
   static constexpr int kStageBytes = kABytes + kBBytes;
@@ -74,9 +77,9 @@ struct Shape {
   static constexpr int kTileFloats = kBM * kBN;
 };
 
-template <int STAGES, int FM>
+template <int STAGES, int FM, int STRIPS = 4>
 constexpr int LdsBytes() {
-  using S = Shape<FM>;
+  using S = Shape<FM, STRIPS>;
   return STAGES * S::kStageBytes > S::kSwapBytes ? STAGES * S::kStageBytes : S::kSwapBytes;
 }
 static_assert(LdsBytes<3, 2>() <= 160 * 1024, "LDS budget");
@@ -285,10 +288,10 @@ __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
 
 // ------------------------------------------------------------- main kernel
 
-template <int STAGES, Epilogue EPI, int FM>
-__global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
+template <int STAGES, Epilogue EPI, int FM, int STRIPS>
+__global__ __launch_bounds__(128 * STRIPS) void GemmKernel(
     GemmParams p, int tiles_m, int band) {
-  using S = Shape<FM>;
+  using S = Shape<FM, STRIPS>;
   extern __shared__ __align__(16) unsigned char lds[];
 
   // XCD-aware remap of the dispatch order, then M-fastest tile order.
@@ -602,10 +605,10 @@ __global__ __launch_bounds__(Shape<FM>::kThreads) void GemmKernel(
 // stored them in, and applies the epilogue. One single-wave work-group per
 // (tile, GEMM wave): each wave's epilogue stands alone, and spreading the
 // partials over that many CUs keeps every CU's share of the reads small.
-template <Epilogue EPI, int FM>
+template <Epilogue EPI, int FM, int STRIPS>
 __global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
                                                        int tiles_m) {
-  using S = Shape<FM>;
+  using S = Shape<FM, STRIPS>;
   constexpr int kQuads = 2 * FM;
   const int tile = blockIdx.x / S::kWaves;
   const int lane = threadIdx.x & 63;
@@ -641,13 +644,14 @@ __global__ __launch_bounds__(64) void SplitReduceKernel(GemmParams p,
   OwnedEpilogue<EPI, FM>(p, own, row0, tile / tiles_m);
 }
 
-template <int STAGES, Epilogue EPI, int FM>
+template <int STAGES, Epilogue EPI, int FM, int STRIPS>
 void Launch(const GemmParams& p, int tiles_m, int band, int groups, hipStream_t stream) {
   const bool reduce = p.splits > 1 && EPI != Epilogue::kPartial;
-  Dispatch(GemmKernel<STAGES, EPI, FM>, dim3(groups), dim3(Shape<FM>::kThreads),
-           LdsBytes<STAGES, FM>(), stream, true, !reduce, p, tiles_m, band);
+  using S = Shape<FM, STRIPS>;
+  Dispatch(GemmKernel<STAGES, EPI, FM, STRIPS>, dim3(groups), dim3(S::kThreads),
+           LdsBytes<STAGES, FM, STRIPS>(), stream, true, !reduce, p, tiles_m, band);
   if (reduce)
-    Dispatch(SplitReduceKernel<EPI, FM>, dim3(groups / p.splits * Shape<FM>::kWaves),
+    Dispatch(SplitReduceKernel<EPI, FM, STRIPS>, dim3(groups / p.splits * S::kWaves),
              dim3(64), 0, stream, false, true, p, tiles_m);
 }
 
@@ -655,9 +659,12 @@ template <Epilogue EPI>
 void LaunchEpi(const GemmParams& p, const GemmPlan& plan, hipStream_t stream) {
   const int groups = plan.tiles * plan.splits;
   if (plan.fm == 2)
-    Launch<3, EPI, 2>(p, (p.m + Shape<2>::kBM - 1) / Shape<2>::kBM, plan.band, groups, stream);
+    Launch<3, EPI, 2, 4>(p, (p.m + Shape<2>::kBM - 1) / Shape<2>::kBM, plan.band, groups, stream);
+  else if (plan.strips == 1)
+    Launch<3, EPI, 1, 1>(p, (p.m + Shape<1, 1>::kBM - 1) / Shape<1, 1>::kBM, plan.band, groups,
+                         stream);
   else
-    Launch<3, EPI, 1>(p, (p.m + Shape<1>::kBM - 1) / Shape<1>::kBM, plan.band, groups, stream);
+    Launch<3, EPI, 1, 4>(p, (p.m + Shape<1>::kBM - 1) / Shape<1>::kBM, plan.band, groups, stream);
 }
 
 }  // namespace
@@ -690,7 +697,16 @@ GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
   const int rounds_wide = (wide + kCus - 1) / kCus;
   const int rounds_tall = (tall + kCus - 1) / kCus;
   plan.fm = epilogue != Epilogue::kPartial && 3 * rounds_tall < 2 * rounds_wide ? 2 : 1;
-  const int bm = plan.fm == 2 ? Shape<2>::kBM : Shape<1>::kBM;
+  // 32-row tiles (one strip per K group) when 128-row tiles would keep
+  // under half the CUs busy and 32-row tiles still fit one round (2 s: 144
+  // rows give q/k/v 64 tiles of 128 rows, the second holding 16 real rows).
+  // Not for split slices: their K split already fills the CUs, and narrow
+  // tiles would leave it no room.
+  const int narrow = (m + Shape<1, 1>::kBM - 1) / Shape<1, 1>::kBM * tiles_n;
+  if (plan.fm == 1 && epilogue != Epilogue::kPartial && 2 * wide < kCus && narrow <= kCus)
+    plan.strips = 1;
+  const int bm = plan.fm == 2 ? Shape<2>::kBM : plan.strips == 1 ? Shape<1, 1>::kBM
+                                                                 : Shape<1>::kBM;
   plan.tiles = (m + bm - 1) / bm * tiles_n;
   plan.stages = 3;
   const int k_steps = k / kBK;
@@ -739,8 +755,10 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
   Require(plan.splits >= 1 && (p.k / kBK) % plan.splits == 0,
           "gemm: K steps not divisible by the split count");
   Require(plan.stages == 3, "gemm: a 3-stage ring");
-  Require(plan.fm == 1 || plan.fm == 2, "gemm: 32- or 64-row strips");
-  const int bm = plan.fm == 2 ? Shape<2>::kBM : Shape<1>::kBM;
+  Require((plan.fm == 1 && (plan.strips == 4 || plan.strips == 1)) ||
+              (plan.fm == 2 && plan.strips == 4),
+          "gemm: 32-row strips by 4 or 1, or 64-row strips by 4");
+  const int bm = 32 * plan.fm * plan.strips;
   Require(plan.tiles == ((p.m + bm - 1) / bm) * ((p.n + kBN - 1) / kBN),
           "gemm: plan does not match the shape");
   Require(p.lda % 8 == 0 && p.ldb % 8 == 0,

@@ -103,7 +103,8 @@ struct GemmParams {
 // floats of `partials` the launch needs.
 struct GemmPlan {
   int stages = 3;  // LDS ring depth
-  int fm = 1;      // strip height in 32-row blocks: tiles of 128 fm rows
+  int fm = 1;      // strip height in 32-row blocks
+  int strips = 4;  // strips per K group: tiles of 32 fm strips rows
   int splits = 1;
   int tiles = 0;
   // Row tiles per band of the tile order: each XCD takes a run of tiles

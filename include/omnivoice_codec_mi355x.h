@@ -38,13 +38,19 @@ typedef struct ovc_config {
 typedef struct ovc_handle ovc_handle;
 
 /* Loads model_root/audio_tokenizer/model.safetensors (float32 tensors under
- * the reference's names, codec.cpp:95-148), or, when model_root is NULL or
- * empty, the seeded synthetic decoder of `weight_seed`. Errors carry the
- * prefix "OmniVoice audio tokenizer: ". Replaces Codec::Load
- * (codec.cpp:92-148), decoder half. */
+ * the reference's names, codec.cpp:95-148); the path is joined as
+ * std::filesystem joins it (NULL or "" names the working directory) and a
+ * missing file is an error. `weight_seed` is unused. Errors carry the prefix
+ * "OmniVoice audio tokenizer: ". Replaces Codec::Load (codec.cpp:92-148),
+ * decoder half. */
 int ovc_create(const ovc_config* config, const char* model_root,
                uint64_t weight_seed, ovc_handle** handle, char* error,
                size_t error_len);
+
+/* The seeded synthetic decoder of `weight_seed` (no reference counterpart:
+ * the benchmark's and the tests' random-init decoder). */
+int ovc_create_synthetic(const ovc_config* config, uint64_t weight_seed,
+                         ovc_handle** handle, char* error, size_t error_len);
 void ovc_destroy(ovc_handle* handle);
 
 /* Samples that `frames` frames decode to. */
@@ -139,13 +145,20 @@ typedef struct ovc_encoder_config {
 typedef struct ovc_encoder ovc_encoder;
 
 /* Loads the encoder half of model_root/audio_tokenizer/model.safetensors
- * (float32 tensors under the reference's names, codec_encoder.cpp:74-240),
- * or, when model_root is NULL or empty, the seeded synthetic encoder of
- * `weight_seed`. Errors carry the prefix "OmniVoice audio tokenizer: ".
- * Replaces LoadEncoder (codec_encoder.cpp:74-240). */
+ * (float32 tensors under the reference's names, codec_encoder.cpp:74-240);
+ * the path is joined as std::filesystem joins it (NULL or "" names the
+ * working directory) and a missing file is an error. `weight_seed` is
+ * unused. Errors carry the prefix "OmniVoice audio tokenizer: ". Replaces
+ * LoadEncoder (codec_encoder.cpp:74-240). */
 int ovc_encoder_create(const ovc_encoder_config* config, const char* model_root,
                        uint64_t weight_seed, ovc_encoder** handle, char* error,
                        size_t error_len);
+
+/* The seeded synthetic encoder of `weight_seed` (no reference counterpart:
+ * the benchmark's and the tests' random-init encoder). */
+int ovc_encoder_create_synthetic(const ovc_encoder_config* config,
+                                 uint64_t weight_seed, ovc_encoder** handle,
+                                 char* error, size_t error_len);
 void ovc_encoder_destroy(ovc_encoder* handle);
 
 /* Codec frames that `samples` input samples encode to. */

@@ -105,19 +105,23 @@ typedef struct ovg_kernel_stat {
 } ovg_kernel_stat;
 
 /* ---- Load (reference: Generator::Load, generator.hpp:22-24, generator.cpp:364-434) ----
- * `model_root` NULL or "" builds the seeded synthetic model: every matrix and
- * embedding drawn from N(0, 0.02) (the counter-based values of
- * ovg_synthetic_values) and rounded to fp16, norms 1.0. A directory holds
- * model.safetensors with the checkpoint's float32 tensors under the names of
- * ovg_host_weights (reference: generator.cpp:377-425); every tensor is found
- * and checked against `config` before the GPU is touched, and errors name
- * the file or tensor at fault. `weight_seed` is then unused. */
+ * Reads model_root/model.safetensors: the checkpoint's float32 tensors under
+ * the names of ovg_host_weights (reference: generator.cpp:377-425). The path
+ * is joined as std::filesystem joins it, so NULL or "" names
+ * model.safetensors in the working directory, as the reference's Load does;
+ * a missing file is an error ("OmniVoice generator: cannot open ..."). Every
+ * tensor is found and checked against `config` before the GPU is touched,
+ * and errors name the file or tensor at fault. `weight_seed` is unused;
+ * synthetic weights come only from ovg_create_synthetic. */
 int ovg_create(const ovg_config* config, const char* model_root,
                uint64_t weight_seed, ovg_handle** handle, char* error,
                size_t error_len);
 
-/* The synthetic model with norm weights 1 + norm_jitter * N(0, 1) (rounded
- * to fp16) instead of 1.0, so that tests see every norm weight. */
+/* The seeded synthetic model: every matrix and embedding drawn from
+ * N(0, 0.02) (the counter-based values of ovg_synthetic_values) and rounded
+ * to fp16; norm weights 1 + norm_jitter * N(0, 1) (rounded to fp16), 1.0 at
+ * norm_jitter 0. No reference counterpart: the benchmark's and the tests'
+ * random-init model. */
 int ovg_create_synthetic(const ovg_config* config, uint64_t weight_seed,
                          float norm_jitter, ovg_handle** handle, char* error,
                          size_t error_len);

@@ -132,6 +132,8 @@ EXPORTS = {
     # the audio decoder (include/omnivoice_codec_mi355x.h)
     "ovc_create": (ctypes.c_int, [ctypes.POINTER(_CodecConfig), ctypes.c_char_p, _u64,
                                   ctypes.POINTER(_ptr), _err, _sz]),
+    "ovc_create_synthetic": (ctypes.c_int, [ctypes.POINTER(_CodecConfig), _u64,
+                                            ctypes.POINTER(_ptr), _err, _sz]),
     "ovc_destroy": (None, [_ptr]),
     "ovc_samples": (_i64, [_ptr, _i64]),
     "ovc_decode": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _err, _sz]),
@@ -147,6 +149,8 @@ EXPORTS = {
     # the audio encoder (include/omnivoice_codec_mi355x.h)
     "ovc_encoder_create": (ctypes.c_int, [ctypes.POINTER(_EncoderConfig), ctypes.c_char_p,
                                           _u64, ctypes.POINTER(_ptr), _err, _sz]),
+    "ovc_encoder_create_synthetic": (ctypes.c_int, [ctypes.POINTER(_EncoderConfig), _u64,
+                                                    ctypes.POINTER(_ptr), _err, _sz]),
     "ovc_encoder_destroy": (None, [_ptr]),
     "ovc_encoder_frames": (_i64, [_ptr, _i64]),
     "ovc_encode": (ctypes.c_int, [_ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _err, _sz]),
@@ -312,13 +316,15 @@ class Generator:
         return cls(h.value, cfg)
 
     @classmethod
-    def load(cls, cfg: dict, model_root: Optional[str] = None,
-             seed: int = 1234) -> "Generator":
+    def load(cls, cfg: dict, model_root: Optional[str] = None) -> "Generator":
+        """Generator::Load: model_root/model.safetensors (None or "" names
+        the working directory, as the reference joins the path; a missing
+        file is an error)."""
         c = _config(cfg)
         h = _ptr()
         err = _buf()
-        root = model_root.encode() if model_root else None
-        _check(lib().ovg_create(ctypes.byref(c), root, seed, ctypes.byref(h),
+        root = (model_root or "").encode()
+        _check(lib().ovg_create(ctypes.byref(c), root, 0, ctypes.byref(h),
                                 err, len(err)), err)
         return cls(h.value, cfg)
 
@@ -552,21 +558,26 @@ class Codec:
         self.cfg = dict(cfg)
 
     @classmethod
-    def load(cls, cfg: dict, model_root: Optional[str] = None,
-             seed: int = 1234) -> "Codec":
-        """model_root/audio_tokenizer/model.safetensors, or the seeded
-        synthetic decoder when model_root is None."""
+    def load(cls, cfg: dict, model_root: Optional[str] = None) -> "Codec":
+        """model_root/audio_tokenizer/model.safetensors (None or "" names the
+        working directory, as the reference joins the path)."""
         c = _codec_config(cfg)
         h = _ptr()
         err = _buf()
-        root = model_root.encode() if model_root else None
-        _check(lib().ovc_create(ctypes.byref(c), root, seed, ctypes.byref(h), err,
+        root = (model_root or "").encode()
+        _check(lib().ovc_create(ctypes.byref(c), root, 0, ctypes.byref(h), err,
                                 len(err)), err)
         return cls(h.value, cfg)
 
     @classmethod
     def synthetic(cls, cfg: dict, seed: int = 1234) -> "Codec":
-        return cls.load(cfg, None, seed)
+        """The seeded synthetic decoder."""
+        c = _codec_config(cfg)
+        h = _ptr()
+        err = _buf()
+        _check(lib().ovc_create_synthetic(ctypes.byref(c), seed, ctypes.byref(h), err,
+                                          len(err)), err)
+        return cls(h.value, cfg)
 
     def samples(self, frames: int) -> int:
         return int(lib().ovc_samples(self._h, frames))
@@ -679,21 +690,27 @@ class Encoder:
         self.cfg = dict(cfg)
 
     @classmethod
-    def load(cls, cfg: dict, model_root: Optional[str] = None,
-             seed: int = 1234) -> "Encoder":
-        """model_root/audio_tokenizer/model.safetensors, or the seeded
-        synthetic encoder when model_root is None."""
+    def load(cls, cfg: dict, model_root: Optional[str] = None) -> "Encoder":
+        """The encoder half of model_root/audio_tokenizer/model.safetensors
+        (None or "" names the working directory, as the reference joins the
+        path)."""
         c = _encoder_config(cfg)
         h = _ptr()
         err = _buf()
-        root = model_root.encode() if model_root else None
-        _check(lib().ovc_encoder_create(ctypes.byref(c), root, seed, ctypes.byref(h), err,
+        root = (model_root or "").encode()
+        _check(lib().ovc_encoder_create(ctypes.byref(c), root, 0, ctypes.byref(h), err,
                                         len(err)), err)
         return cls(h.value, cfg)
 
     @classmethod
     def synthetic(cls, cfg: dict, seed: int = 1234) -> "Encoder":
-        return cls.load(cfg, None, seed)
+        """The seeded synthetic encoder."""
+        c = _encoder_config(cfg)
+        h = _ptr()
+        err = _buf()
+        _check(lib().ovc_encoder_create_synthetic(ctypes.byref(c), seed, ctypes.byref(h),
+                                                  err, len(err)), err)
+        return cls(h.value, cfg)
 
     def frames(self, samples: int) -> int:
         return int(lib().ovc_encoder_frames(self._h, samples))

@@ -85,8 +85,9 @@ Generator::~Generator() = default;
 std::unique_ptr<Generator> Generator::Load(const Config& config,
                                            const std::filesystem::path& model_root,
                                            std::string* error) {
-  if (model_root.empty())
-    return LoadSynthetic(config, 1234, error);
+  // model_root / "model.safetensors" (an empty root names the working
+  // directory, as in the reference); synthetic weights only through
+  // LoadSynthetic.
   const ovg_config c = ToC(config);
   char message[kMessage] = {};
   auto state = std::make_unique<State>();

@@ -158,10 +158,12 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
   const uint32_t v_lane = static_cast<uint32_t>(
       (lane >> 2) * p.ldvt + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
   const uint32_t lds_base = LdsAddress(lds);
-  // The r-th round processed is key round (r + shift) % rounds: work-groups
-  // of the same head start on different rounds, so they do not all pull the
-  // same L2 lines at once. Its tiles go to ring half r % 2.
-  const int shift = (blockIdx.x / p.kv_heads) % rounds;
+  // The r-th round processed is key round (r + shift) % rounds: the query
+  // tiles of a sequence start on different rounds, so they do not all pull
+  // the same L2 lines at once. Its tiles go to ring half r % 2. The shift
+  // is the query tile's index inside its own sequence, so a query's order of
+  // accumulation does not depend on what else is packed in the batch.
+  const int shift = ((work.q_begin - work.seq_begin) / kKTile) % rounds;
   auto round_of = [&](int r) {
     const int k = r + shift;
     return k >= rounds ? k - rounds : k;

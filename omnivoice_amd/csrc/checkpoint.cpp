@@ -218,6 +218,12 @@ std::size_t DTypeBytes(const std::string& dtype) {
 
 }  // namespace
 
+std::string JoinPath(const std::string& root, const std::string& name) {
+  if (root.empty())
+    return name;
+  return root.back() == '/' ? root + name : root + "/" + name;
+}
+
 std::unique_ptr<SafetensorsFile> SafetensorsFile::Open(const std::string& path) {
   std::unique_ptr<SafetensorsFile> file(new SafetensorsFile());
   file->path_ = path;

@@ -16,6 +16,10 @@
 
 namespace ovg {
 
+// `root` / `name` as std::filesystem::path joins them: an empty root gives
+// `name` itself (relative to the working directory).
+std::string JoinPath(const std::string& root, const std::string& name);
+
 // A read-only mapping of one safetensors file. Open and F32 throw ovg::Error
 // with a message naming the file or tensor at fault.
 class SafetensorsFile {

@@ -16,9 +16,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
-// Rows of every activation buffer are padded to this multiple (plus one
-// 32-row key tile of slack) so tile loads never leave the allocation.
-constexpr int kRowAlign = 256;
 // Each packed sequence starts at a multiple of this many rows, so that its
 // 32-key tiles of V^T start on whole 16-row blocks (see VtColumn).
 constexpr int kSequenceAlign = 16;

@@ -1019,12 +1019,25 @@ int ovc_encoder_create(const ovc_encoder_config* config, const char* model_root,
   return ovg::CodecGuard("OmniVoice audio tokenizer: ", error, error_len, [&] {
     ovg::Require(config != nullptr && handle != nullptr, "null argument");
     CheckEncoderConfig(*config);
-    std::unique_ptr<ovg::SafetensorsFile> file;
-    if (model_root != nullptr && model_root[0] != '\0')
-      file = ovg::SafetensorsFile::Open(std::string(model_root) +
-                                        "/audio_tokenizer/model.safetensors");
+    // model_root / "audio_tokenizer/model.safetensors", as std::filesystem
+    // joins it (an empty root names the working directory); synthetic
+    // weights come only from the *_create_synthetic entry point.
+    std::unique_ptr<ovg::SafetensorsFile> file = ovg::SafetensorsFile::Open(ovg::JoinPath(
+        model_root == nullptr ? "" : model_root, "audio_tokenizer/model.safetensors"));
     auto h = std::make_unique<ovc_encoder>();
     h->engine = std::make_unique<ovg::EncoderEngine>(*config, weight_seed, file.get());
+    *handle = h.release();
+    return OVG_OK;
+  });
+}
+
+int ovc_encoder_create_synthetic(const ovc_encoder_config* config, uint64_t weight_seed,
+                                 ovc_encoder** handle, char* error, size_t error_len) {
+  return ovg::CodecGuard("OmniVoice audio tokenizer: ", error, error_len, [&] {
+    ovg::Require(config != nullptr && handle != nullptr, "null argument");
+    CheckEncoderConfig(*config);
+    auto h = std::make_unique<ovc_encoder>();
+    h->engine = std::make_unique<ovg::EncoderEngine>(*config, weight_seed, nullptr);
     *handle = h.release();
     return OVG_OK;
   });

@@ -31,10 +31,11 @@
 // of one output).
 //
 // Split-K: with the kPartial epilogue every split stores its own fp32 slice
-// and the row kernel that consumes the output sums the slices. Otherwise
-// (small M only) each split stores its owned values as a partial and a
-// second launch sums the partials in split order 0, 1, ... and runs the same
-// epilogue; the kernel boundary publishes the partials to every XCD.
+// and the row kernel that consumes the output sums the slices; the split
+// count depends on K only. Otherwise (stand-alone calls at small M only)
+// each split stores its owned values as a partial and a second launch sums
+// the partials in split order 0, 1, ... and runs the same epilogue; the
+// kernel boundary publishes the partials to every XCD.
 //
 // Work-groups are dispatched round-robin over the 8 XCDs; the block index is
 // remapped so that each XCD receives a contiguous run of tiles, ordered
@@ -684,67 +685,65 @@ int BandFor(int m, int k, int bm, int splits) {
       1, std::min<std::int64_t>(tiles_m, kBandBytes / row_tile_bytes)));
 }
 
-GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue) {
+// Split count of the partial-slice GEMMs (o and down): a function of K
+// alone, so that a row's slices, and the order in which the row kernel sums
+// them, are the same whatever else is packed in the batch. Four slices where
+// each keeps at least two K steps (the released o and down: 8 and 12 steps
+// per slice), else three or two.
+int PartialSplits(int k_steps) {
+  for (const int s : {4, 3, 2})
+    if (k_steps % s == 0 && k_steps / s >= 2)
+      return s;
+  return 1;
+}
+
+GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue, bool split_small) {
   GemmPlan plan;
   const int tiles_n = (n + kBN - 1) / kBN;
-  // 256-row tiles when they take fewer rounds of work-groups over the CUs,
-  // counting a 256-row tile as 1.5 128-row tiles (twice the MFMAs at a
-  // quarter less LDS traffic and fill per MFMA, the same fixed costs):
-  // large M, and shapes whose 128-row tiles spill a few work-groups into a
-  // second round (the audio heads at 500 rows: 260 tiles).
-  const int wide = (m + Shape<1>::kBM - 1) / Shape<1>::kBM * tiles_n;
-  const int tall = (m + Shape<2>::kBM - 1) / Shape<2>::kBM * tiles_n;
+  const int k_steps = k / kBK;
+  const bool partial = epilogue == Epilogue::kPartial;
+  const int splits = partial ? PartialSplits(k_steps) : 1;
+  // Tile height from the work-group counts (tiles x splits). 256-row tiles
+  // when they take fewer rounds of work-groups over the CUs, counting a
+  // 256-row tile as 1.5 128-row tiles (twice the MFMAs at a quarter less LDS
+  // traffic and fill per MFMA, the same fixed costs): large M, and shapes
+  // whose 128-row tiles spill a few work-groups into a second round (the
+  // audio heads at 500 rows: 260 tiles).
+  const int wide = (m + Shape<1>::kBM - 1) / Shape<1>::kBM * tiles_n * splits;
+  const int tall = (m + Shape<2>::kBM - 1) / Shape<2>::kBM * tiles_n * splits;
   const int rounds_wide = (wide + kCus - 1) / kCus;
   const int rounds_tall = (tall + kCus - 1) / kCus;
-  plan.fm = epilogue != Epilogue::kPartial && 3 * rounds_tall < 2 * rounds_wide ? 2 : 1;
+  plan.fm = 3 * rounds_tall < 2 * rounds_wide ? 2 : 1;
   // 32-row tiles (one strip per K group) when 128-row tiles would keep
-  // under half the CUs busy and 32-row tiles still fit one round (2 s: 144
-  // rows give q/k/v 64 tiles of 128 rows, the second holding 16 real rows).
-  // Not for split slices: their K split already fills the CUs, and narrow
-  // tiles would leave it no room.
-  const int narrow = (m + Shape<1, 1>::kBM - 1) / Shape<1, 1>::kBM * tiles_n;
-  if (plan.fm == 1 && epilogue != Epilogue::kPartial && 2 * wide < kCus && narrow <= kCus)
+  // under half the CUs busy and 32-row tiles still fit one round (2 s: the
+  // packed 144 rows give q/k/v 64 tiles of 128 rows, the second holding 16
+  // real rows).
+  const int narrow = (m + Shape<1, 1>::kBM - 1) / Shape<1, 1>::kBM * tiles_n * splits;
+  if (plan.fm == 1 && 2 * wide < kCus && narrow <= kCus)
     plan.strips = 1;
   const int bm = plan.fm == 2 ? Shape<2>::kBM : plan.strips == 1 ? Shape<1, 1>::kBM
                                                                  : Shape<1>::kBM;
   plan.tiles = (m + bm - 1) / bm * tiles_n;
   plan.stages = 3;
-  const int k_steps = k / kBK;
-  int splits = 1;
-  if (epilogue == Epilogue::kPartial) {
-    // Split slices are summed by the row kernel that reads the output
-    // anyway: split until the grid covers most CUs, keeping >= 8 K steps
-    // per split for the DMA ring to overlap, or >= 4 while the grid stays
-    // within half the CUs (small M, where more work-groups pulling operands
-    // win over a full ring). Never past one work-group per CU: a second
-    // round of work-groups costs more than the longer K loop of fewer
-    // splits.
+  plan.splits = splits;
+  plan.partial_floats = 0;
+  // The generator never splits the other GEMMs: a split chosen from M would
+  // make a row's sums depend on the batch. Stand-alone callers may split K
+  // when the tiles leave most CUs idle (partials cost a round trip through
+  // memory and a second launch that sums them in split order).
+  if (!partial && split_small && plan.tiles < 64) {
+    int s_best = 1;
     for (const int s : {2, 3, 4, 6, 8}) {
-      if (plan.tiles * splits >= 160 || plan.tiles * s > kCus)
-        break;
-      const int min_steps = plan.tiles * s <= 128 ? 4 : 8;
-      if (k_steps % s == 0 && k_steps / s >= min_steps)
-        splits = s;
-    }
-    plan.splits = splits;
-    plan.partial_floats = 0;
-    plan.band = BandFor(m, k, bm, splits);
-    return plan;
-  }
-  // Otherwise split K only when the tiles leave most CUs idle; partials
-  // cost a round trip through memory and a second launch.
-  if (plan.tiles < 64) {
-    for (const int s : {2, 3, 4, 6, 8}) {
-      if (plan.tiles * splits >= 128)
+      if (plan.tiles * s_best >= 128)
         break;
       if (k_steps % s == 0 && k_steps / s >= 4)
-        splits = s;
+        s_best = s;
     }
+    plan.splits = s_best;
+    plan.partial_floats =
+        s_best > 1 ? static_cast<std::size_t>(plan.tiles) * s_best * bm * kBN : 0;
   }
-  plan.splits = splits;
-  plan.partial_floats =
-      splits > 1 ? static_cast<std::size_t>(plan.tiles) * splits * bm * kBN : 0;
-  plan.band = BandFor(m, k, bm, splits);
+  plan.band = BandFor(m, k, bm, plan.splits);
   return plan;
 }
 

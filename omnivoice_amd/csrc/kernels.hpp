@@ -114,7 +114,11 @@ struct GemmPlan {
   int band = 0;
   std::size_t partial_floats = 0;
 };
-GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue);
+// The tile shape and split count of one GEMM. The split count of the
+// partial-slice epilogue depends on K only, and no other epilogue is split
+// unless `split_small` asks for it (stand-alone calls), so the generator's
+// per-row results do not depend on the packed row count M.
+GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue, bool split_small = false);
 void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
                 hipStream_t stream);
 

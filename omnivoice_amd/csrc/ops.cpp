@@ -139,7 +139,7 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
     const auto epi =
         accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;
     const ovg::GemmPlan plan = ovg::PlanGemm(
-        static_cast<int>(rows), static_cast<int>(out), static_cast<int>(in), epi);
+        static_cast<int>(rows), static_cast<int>(out), static_cast<int>(in), epi, true);
     Scratch<float> partials(plan.partial_floats);
     ovg::GemmParams p{};
     p.x = static_cast<const ovg::half_t*>(x);

@@ -465,6 +465,9 @@ Layout Engine::Plan(const std::vector<Input>& inputs) const {
     L.max_total = std::max(L.max_total, static_cast<int>(C * in.frames));
   }
   L.rows = row;
+  // One 32-row key tile of slack past the last sequence: attention reads
+  // whole key tiles. GEMM operand loads clamp their rows to M - 1, so they
+  // need no slack.
   L.rows_alloc = row + 32;
   L.targets = logit_row;
   L.outputs = out_base;
@@ -1057,17 +1060,17 @@ int Guard(const char* prefix, char* error, std::size_t len, F&& body) {
 extern "C" {
 
 int ovg_create(const ovg_config* config, const char* model_root,
-               uint64_t weight_seed, ovg_handle** handle, char* error,
+               uint64_t /*weight_seed*/, ovg_handle** handle, char* error,
                size_t error_len) {
-  if (model_root == nullptr || model_root[0] == '\0')
-    return ovg_create_synthetic(config, weight_seed, 0.0F, handle, error,
-                                error_len);
   return Guard("OmniVoice generator: ", error, error_len, [&] {
     ovg::Require(config != nullptr && handle != nullptr, "null argument");
     // Every tensor is located and checked against the config before the GPU
     // is touched (reference: generator.cpp:364-434 reads the same names).
-    const auto file = ovg::SafetensorsFile::Open(std::string(model_root) +
-                                                 "/model.safetensors");
+    // The file is model_root / "model.safetensors" as std::filesystem joins
+    // it: an empty root names model.safetensors in the working directory,
+    // which the reference's Load tries too and fails on when it is absent.
+    const auto file = ovg::SafetensorsFile::Open(
+        ovg::JoinPath(model_root == nullptr ? "" : model_root, "model.safetensors"));
     const ovg_config& c = *config;
     const std::int64_t h = c.hidden_size, q_rows = c.heads * c.head_dim,
                        kv_rows = c.kv_heads * c.head_dim,

@@ -19,6 +19,14 @@
  *   orc_forward pieces   - float64 textbook formulas at tiny shapes and the
  *                          installed transformers Qwen3 layer (fixtures).
  *   orc_synth_*          - numpy float16 rounding; closed-form moments.
+ *   orc_model_from_host  - the synthetic model's tensors in the reference's
+ *                          load layout give the synthetic model's logits bit
+ *                          for bit; swapped gate/up or k/v do not.
+ *   orc_generate         - the loop spelled out from the pinned forward,
+ *                          score and oracle/_ref's PositionSelector, with the
+ *                          write-back into the conditional target frames.
+ *   orc_generate_from_logits
+ *                        - score + the selector step by step.
  *   orc_conv1d, orc_conv_transpose1d, orc_snake
  *                        - torch.nn.functional.conv1d / conv_transpose1d
  *                          in float64 on the CPU, and the Snake closed form.

@@ -119,6 +119,9 @@ int main() {
   Expect(!ov::Generator::Load(config, "/nonexistent/checkpoint", &error) &&
              error.rfind("OmniVoice generator: ", 0) == 0,
          "a missing checkpoint is an error with the generator prefix");
+  Expect(!ov::Generator::Load(config, "", &error) &&
+             error.rfind("OmniVoice generator: cannot open model.safetensors", 0) == 0,
+         "an empty model root is an open error, not a synthetic model");
 
   std::cout << (failures == 0 ? "ok" : "FAIL") << " generator: " << failures
             << " failures\n";

@@ -79,6 +79,26 @@ def test_missing_checkpoint_directory_is_an_error():
     assert str(e.value).startswith("OmniVoice generator: ")
 
 
+@pytest.mark.parametrize("root", [None, ""])
+def test_empty_checkpoint_root_is_an_error(root, tmp_path, monkeypatch):
+    """An empty model root names model.safetensors in the working directory,
+    as the reference's Load joins model_root / "model.safetensors"
+    (generator.cpp:371-374): with no such file every loader fails with its
+    prefix instead of building synthetic weights."""
+    monkeypatch.chdir(tmp_path)
+    with pytest.raises(ov.GeneratorError,
+                       match="^OmniVoice generator: cannot open model.safetensors"):
+        ov.Generator.load(ov.released_config(), root)
+    with pytest.raises(ov.GeneratorError,
+                       match="^OmniVoice audio tokenizer: cannot open "
+                             "audio_tokenizer/model.safetensors"):
+        ov.Codec.load(ov.codec_released_config(), root)
+    with pytest.raises(ov.GeneratorError,
+                       match="^OmniVoice audio tokenizer: cannot open "
+                             "audio_tokenizer/model.safetensors"):
+        ov.Encoder.load(ov.encoder_released_config(), root)
+
+
 def test_build_input_rejects_bad_arguments():
     ids = np.zeros(8, dtype=np.int32)
     assert ov.lib().ovg_build_input(None, -1, None, 0, 1, 8, 1024,

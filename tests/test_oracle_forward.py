@@ -125,3 +125,88 @@ def test_emulated_fp16_stays_close_to_float32():
     a = model.forward(ids, case["audio_start"], case["target"], emulate=False)
     b = model.forward(ids, case["audio_start"], case["target"], emulate=True)
     assert 0 < np.abs(a - b).max() < 5e-3
+
+
+def _host_tensors(cfg, seed, jitter):
+    """The synthetic model's values as host float32 tensors in the layout
+    orc_model_from_host takes (the reference's Load order: text, audio
+    embeddings, audio heads, final norm, then per layer q, k, v, o, gate, up,
+    down, input norm, post norm, q norm, k norm), drawn with the oracle's own
+    generator."""
+    h, i = cfg["hidden_size"], cfg["intermediate_size"]
+    q, kv, d = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["head_dim"]
+    audio_rows = cfg["audio_codebooks"] * cfg["audio_vocab_size"]
+
+    def values(tensor, shape, norm=False):
+        out = np.zeros(int(np.prod(shape)), dtype=np.float32)
+        oracle.lib().orc_synth_values(seed, tensor, 0, out.size, int(norm), jitter,
+                                      out.ctypes.data)
+        return out.reshape(shape)
+
+    shapes = [(q, h), (kv, h), (kv, h), (h, q), (i, h), (i, h), (h, i),
+              (h,), (h,), (d,), (d,)]
+    layers = [[values(100 + 16 * l + k, shape, k >= 7) for k, shape in enumerate(shapes)]
+              for l in range(cfg["layers"])]
+    return {"text": values(1, (cfg["vocab_size"], h)),
+            "audio_embeddings": values(2, (audio_rows, h)),
+            "audio_heads": values(3, (audio_rows, h)),
+            "final_norm": values(4, (h,), True), "layers": layers}
+
+
+def test_model_from_host_matches_synthetic_model():
+    """orc_model_from_host (generator.cpp:364-425 layout: q|k|v and gate|up
+    fused in that order) given the synthetic model's tensors gives the
+    synthetic model's logits bit for bit; the synthetic model is pinned by
+    the transformers fixture above. Swapping gate and up, or k and v, moves
+    the logits, so the fused order is what is checked."""
+    from conftest import random_input, tiny_config
+    cfg = tiny_config()
+    host = _host_tensors(cfg, 21, 0.1)
+    synthetic = oracle.Model(cfg, 21, 0.1)
+    loaded = oracle.Model(cfg, host=host)
+    rng = np.random.default_rng(3)
+    ids = random_input(rng, cfg, 7, 5, 19, 0.3)
+    for emulate in (False, True):
+        a = synthetic.forward(ids, 7, 19, emulate=emulate)
+        b = loaded.forward(ids, 7, 19, emulate=emulate)
+        assert a.tobytes() == b.tobytes()
+    for x, y in [(4, 5), (1, 2)]:
+        bad = dict(host, layers=[list(layer) for layer in host["layers"]])
+        bad["layers"][0][x], bad["layers"][0][y] = bad["layers"][0][y], bad["layers"][0][x]
+        swapped = oracle.Model(cfg, host=bad).forward(ids, 7, 19)
+        assert np.abs(swapped - synthetic.forward(ids, 7, 19)).max() > 1e-3
+
+
+@pytest.mark.parametrize("temperature,seed,target", [(0.0, 0, 12), (5.0, 42, 12), (5.0, 7, 3)])
+def test_closed_loop_generate_matches_stepwise_loop(temperature, seed, target):
+    """orc_generate (the closed loop of generator.cpp:486-543) equals the loop
+    spelled out step by step from pinned pieces: the forward, the score and
+    the reference's own compiled PositionSelector (oracle/_ref, when built;
+    the oracle's selector, pinned against it, otherwise), writing each step's
+    chosen codes into the conditional target frames (generator.cpp:526-535)
+    and skipping zero-count steps."""
+    from conftest import random_input, tiny_config
+    cfg = tiny_config()
+    model = oracle.Model(cfg, 21, 0.1)
+    rng = np.random.default_rng(seed + 5)
+    text, ref = 6, 4
+    ids = random_input(rng, cfg, text, ref, target)
+    codes, at = model.generate(ids, text, target, temperature=temperature, seed=seed)
+    sel = oracle.Selector(5.0, temperature, seed, use_ref=oracle.ref_available())
+    current = ids.copy()
+    expect = np.full(8 * target, 1024, dtype=np.int32)
+    expect_at = np.full(8 * target, -1, dtype=np.int32)
+    steps = 0
+    for step, count in enumerate(oracle.unmask_schedule(8 * target, 32, 0.1)):
+        if count == 0:
+            continue
+        steps += 1
+        logits = model.forward(current, text, target)
+        pred, conf = oracle.score(logits, target, 8, 1025, 1024, 2.0)
+        for i in sel.fill(count, 8, target, pred, conf, 1024, expect):
+            expect_at[i] = step
+        current[:, -target:] = expect.reshape(8, target)
+    assert steps == (32 if target == 12 else 24)  # 24 positions leave 8 steps empty
+    np.testing.assert_array_equal(codes.ravel(), expect)
+    np.testing.assert_array_equal(at.ravel(), expect_at)
+    assert (codes != 1024).all()

@@ -6,12 +6,13 @@ Metric: utterance RTF + unmask steps/s for a 10 s utterance (250 frames at
 backbone with seeded random fp16 weights (synthetic; no checkpoint) and
 seeded Gumbel position noise at temperature 5.0.
 
-A benchmark "step" is one whole utterance: Generator::Generate, i.e. 32
+`--steps K` times K whole utterances: Generator::Generate, i.e. 32
 unmasking steps (forward of the packed CFG batch, CFG scoring, top-k
 selection) with the inputs already resident on the device and only the
 final codes copied back. `value` is unmask steps per second
-(32 x utterances / wall time); `utterance_rtf` is wall time per utterance
-over 10 s.
+(32 x utterances / wall time), `ms_per_step` milliseconds per unmasking
+step, `ms_per_utterance` per whole utterance, and `utterance_rtf` wall time
+per utterance over its seconds of audio.
 
 Other workloads (--workload): 2s, clone (5 s reference voice + 15 s target)
 and chunks (four 15 s chunks of long text generated as one batch through
@@ -20,8 +21,10 @@ items and `utterance_rtf` is wall time over the 60 s of audio).
 
 Also reported: the roofline of the dominant kernel (algorithmic FLOPs or
 bytes per launch over its HIP-event-timed launch duration on the library
-stream) and the CPU baseline (the oracle's float32 restatement of the
-reference's path, one unmasking step of the same workload on the host).
+stream, against the bound its arithmetic intensity sets), the algorithmic
+HBM bytes of a whole step against its time, and the CPU baseline (the
+oracle's float32 restatement of the reference's path, whole unmasking steps
+of the same workload on the host's CPUs).
 """
 import argparse
 import json
@@ -47,6 +50,12 @@ WORKLOADS = {
     "chunks": (110, 0, 375),
 }
 ITEMS = {"chunks": 4}  # items generated together (ovg_generate_batch)
+DESCRIPTIONS = {
+    "10s": "10 s speech",
+    "2s": "2 s speech",
+    "clone": "15 s speech cloning a 5 s reference",
+    "chunks": "4 x 15 s chunks of long text batched",
+}
 
 
 def make_input(ov, text, reference, target, seed=42):
@@ -56,11 +65,30 @@ def make_input(ov, text, reference, target, seed=42):
     return ov.ConditionalInput.build(tokens, refc, reference, target)
 
 
-def cpu_baseline(cfg, x, decoding, steps):
-    """The oracle (float32, all host threads up to 16) timed on `steps`
-    unmasking steps of the workload: forward, score and select."""
+def host_cpu():
+    """(model name, logical CPUs this process may run on, threads to use):
+    every CPU in the affinity mask, capped by OMP_NUM_THREADS where it is set
+    (a one-GPU box's share of the host, 16)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    available = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return model, available, min(available, cap) if cap > 0 else available
+
+
+def cpu_baseline(cfg, x, decoding, min_seconds):
+    """The oracle (float32) timed on whole unmasking steps of the workload
+    (forward, score and select), as many as fit `min_seconds` (at least
+    two), on every CPU of this process's share of the host."""
     import oracle
-    threads = min(16, os.cpu_count() or 1)
+    model_name, available, threads = host_cpu()
     oracle.lib().orc_set_threads(threads)
     t0 = time.perf_counter()
     model = oracle.Model(cfg, 1234)
@@ -69,19 +97,24 @@ def cpu_baseline(cfg, x, decoding, steps):
     C, F, V = 8, x.target_frames, 1025
     sel = oracle.Selector(decoding.layer_penalty, decoding.position_temperature, 42)
     codes = np.full(C * F, 1024, dtype=np.int32)
-    schedule = oracle.unmask_schedule(C * F, 32, decoding.t_shift)
+    schedule = [c for c in oracle.unmask_schedule(C * F, 32, decoding.t_shift) if c]
     t0 = time.perf_counter()
-    for s in range(steps):
+    steps = 0
+    while steps < len(schedule) and (steps < 2 or time.perf_counter() - t0 < min_seconds):
         logits = model.forward(ids, x.audio_start, F)
         pred, conf = oracle.score(logits, F, C, V, 1024, decoding.guidance)
-        sel.fill(schedule[s], C, F, pred, conf, 1024, codes)
+        sel.fill(schedule[steps], C, F, pred, conf, 1024, codes)
+        ids[:, -F:] = codes.reshape(C, F)
+        steps += 1
     elapsed = time.perf_counter() - t0
     return {"value": steps / elapsed, "unit": "unmask steps/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{steps} unmasking step(s) of the {F}-frame workload "
-                      f"(forward of {x.length + F} packed rows, score, select), "
-                      f"float32 oracle; weight synthesis {setup:.1f} s excluded",
-            "utterance_rtf_extrapolated": (elapsed / steps * 32) / (F / 25.0)}
+            "kind": "port", "cpu_model": model_name, "cpus_available": available,
+            "sample": f"the first {steps} of the {len(schedule)} unmasking steps of one "
+                      f"{F}-frame utterance (forward of {x.length + F} packed rows, score, "
+                      f"select, write-back), float32 oracle on {threads} threads of "
+                      f"{model_name}, {elapsed:.1f} s; weight synthesis {setup:.1f} s "
+                      f"excluded",
+            "utterance_rtf_extrapolated": (elapsed / steps * len(schedule)) / (F / 25.0)}
 
 
 def bench_codec(args, torch):
@@ -133,9 +166,9 @@ def bench_codec(args, torch):
         "decode_tflops": total_flops / (elapsed / args.steps) / 1e12,
         "kernels": kernels,
     }
-    if args.cpu_steps > 0:
+    if args.cpu_seconds > 0:
         import oracle
-        threads = min(16, os.cpu_count() or 1)
+        model_name, _, threads = host_cpu()
         oracle.lib().orc_set_threads(threads)
         model = oracle.Codec(oracle.codec_released_config(), 1234)
         sample = codes_host[:, :25]
@@ -143,7 +176,7 @@ def bench_codec(args, torch):
         model.decode(sample)
         cpu = time.perf_counter() - t0
         result["cpu_baseline"] = {"value": 1.0 / cpu, "unit": "audio seconds decoded per second",
-                                  "cores": threads, "kind": "port",
+                                  "cores": threads, "kind": "port", "cpu_model": model_name,
                                   "sample": "1 s (25 frames) decoded by the float32 oracle "
                                             "(double sums); table synthesis excluded"}
     print(json.dumps(result), flush=True)
@@ -205,9 +238,9 @@ def bench_encode(args, torch):
         "encode_tflops": total_flops / (elapsed / args.steps) / 1e12,
         "kernels": kernels,
     }
-    if args.cpu_steps > 0:
+    if args.cpu_seconds > 0:
         import oracle
-        threads = min(16, os.cpu_count() or 1)
+        model_name, _, threads = host_cpu()
         oracle.lib().orc_set_threads(threads)
         model = oracle.Encoder(oracle.encoder_released_config(), 1234)
         sample = host[:24000]
@@ -215,7 +248,7 @@ def bench_encode(args, torch):
         model.encode(sample)
         cpu = time.perf_counter() - t0
         result["cpu_baseline"] = {"value": 1.0 / cpu, "unit": "audio seconds encoded per second",
-                                  "cores": threads, "kind": "port",
+                                  "cores": threads, "kind": "port", "cpu_model": model_name,
                                   "sample": "1 s (25 frames) encoded by the float32 oracle "
                                             "(double sums); weight synthesis excluded"}
     print(json.dumps(result), flush=True)
@@ -267,11 +300,13 @@ def gemm_compare(args, torch):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=60,
+                    help="utterances timed (each one Generate call of 32 unmasking steps)")
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="10s", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-steps", type=int, default=2,
-                    help="unmasking steps timed for the CPU baseline (0 skips it)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="seconds of whole unmasking steps timed for the CPU baseline "
+                         "(0 skips it)")
     ap.add_argument("--profile-repeats", type=int, default=3)
     ap.add_argument("--codec", action="store_true",
                     help="benchmark the audio decoder on the workload's frames instead")
@@ -362,25 +397,32 @@ def main():
     dominant = max(stats, key=lambda n: stats[n]["total_ms"])
     d = stats[dominant]
     per_launch_ms = d["total_ms"] / d["launches"]
-    if d["flops"]:
+    # The bound is the one the kernel's arithmetic intensity puts it under:
+    # below the ridge point (peak FLOP/s over peak bytes/s, 312.5 FLOP/B)
+    # HBM, above it the matrix cores (the 2 s workload's GEMMs stream their
+    # weights; the 10 s, clone and chunk GEMMs are compute-bound).
+    intensity = d["flops"] / d["bytes"] if d["bytes"] else float("inf")
+    ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if d["flops"] and intensity >= ridge:
         achieved = d["flops"] / d["launches"] / (per_launch_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": achieved / PEAK_FP16_TFLOPS,
-                    "traffic": None, "kernel": dominant,
-                    "avg_launch_us": per_launch_ms * 1e3}
+                    "unit": "TFLOP/s", "frac": achieved / PEAK_FP16_TFLOPS}
     else:
         achieved = d["bytes"] / d["launches"] / (per_launch_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
-                    "traffic": None, "kernel": dominant,
-                    "avg_launch_us": per_launch_ms * 1e3}
+                    "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS}
+    roofline.update({"traffic": None, "kernel": dominant,
+                     "avg_launch_us": per_launch_ms * 1e3,
+                     "algorithmic_flops": d["flops"] / d["launches"],
+                     "algorithmic_bytes": d["bytes"] / d["launches"],
+                     "intensity_flop_per_byte": intensity})
     # HBM bytes per launch of the dominant kernel, from the calibrated
     # FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/.
     traffic_path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     if os.path.exists(traffic_path):
         with open(traffic_path) as f:
-            measured = json.load(f).get(dominant)
-        if measured and measured.get("workload") == args.workload:
+            measured = json.load(f).get(args.workload, {}).get(dominant)
+        if measured:
             roofline["traffic"] = measured["bytes"]
             roofline["traffic_source"] = "profiles/" + measured["source"]
     gemm_ms = sum(s["total_ms"] for n, s in stats.items() if n.startswith("gemm_")
@@ -388,14 +430,23 @@ def main():
     gemm_flops = sum(s["flops"] for n, s in stats.items() if n.startswith("gemm_")
                      and n != "gemm_audio_heads")
 
+    # Algorithmic HBM bytes of one unmasking step: every fp16 weight once,
+    # the logits written once and the embedding rows in and out.
+    step_bytes = sum(s["bytes"] for s in stats.values()) / args.profile_repeats
+    ms_per_unmask_step = elapsed / (args.steps * executed) * 1e3
     result = {
-        "metric": "utterance RTF + unmask steps/s, 10 s speech, 32 steps, CFG 2.0, 1 GPU",
+        "metric": f"utterance RTF + unmask steps/s, {DESCRIPTIONS[args.workload]}, "
+                  f"32 steps, CFG 2.0, 1 GPU",
         "value": steps_per_s,
         "unit": "unmask steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_utterance,
+        "ms_per_step": ms_per_unmask_step,
+        "step_unit": f"ms_per_step is per unmasking step (one forward of the packed batch, "
+                     f"CFG score and top-k select); --steps counts utterances of "
+                     f"{executed} unmasking steps each",
+        "ms_per_utterance": ms_per_utterance,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -420,11 +471,14 @@ def main():
         "roofline": roofline,
         "backbone_gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
         "eager_step_ms": total_ms / args.profile_repeats,
+        "step_hbm": {"algorithmic_bytes": step_bytes,
+                     "achieved_gbs": step_bytes / (ms_per_unmask_step * 1e-3) / 1e9,
+                     "frac": step_bytes / (ms_per_unmask_step * 1e-3) / 1e9 / PEAK_HBM_GBS},
         "kernels": kernels,
         "load_s": load_s,
     }
-    if args.cpu_steps > 0 and items == 1:
-        result["cpu_baseline"] = cpu_baseline(cfg, x, decoding, args.cpu_steps)
+    if args.cpu_seconds > 0 and items == 1:
+        result["cpu_baseline"] = cpu_baseline(cfg, x, decoding, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

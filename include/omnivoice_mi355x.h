@@ -159,15 +159,39 @@ int ovg_generate(ovg_handle* handle, const ovg_input* input,
                  int32_t* unmasked_at, char* error, size_t error_len);
 
 /* Several independent inputs (e.g. chunks of a long text) generated in one
- * packed batch; item i uses seeds[i] and writes codes[i] / unmasked_at[i].
- * Equivalent to calling ovg_generate per item (reference: the sequential
- * chunk loop at synthesizer.cpp:179-201 calls Generate once per chunk). */
+ * packed batch; item i uses seeds[i] and writes codes[i] / unmasked_at[i],
+ * bit for bit what ovg_generate gives for the item alone (reference: the
+ * sequential chunk loop at synthesizer.cpp:179-201 calls Generate once per
+ * chunk): no kernel's order of summation depends on the other items. */
 int ovg_generate_batch(ovg_handle* handle, int64_t count,
                        const ovg_input* inputs, const ovg_decoding* decoding,
                        const uint64_t* seeds, int (*cancelled)(void* user),
                        void* user, int32_t* const* codes,
                        int32_t* const* unmasked_at, char* error,
                        size_t error_len);
+
+/* ---- The chunk loop of Synthesizer::Synthesize (reference: synthesizer.cpp:179-201) ----
+ * Generates the `count` chunks of one long text with one seed, with the
+ * results of the reference's loop, which calls Generate once per chunk
+ * (synthesizer.cpp:70-71): chunk i's input is ConditionalInput::Build(
+ * text_ids[i], reference, target_frames[i]) (decoding.cpp:42-62). With a
+ * reference voice (reference_frames > 0, reference_codes [codebooks]
+ * [reference_frames]) every chunk is conditioned on it and all chunks run as
+ * one packed batch. Without one, chunk 0 runs alone and its codes become the
+ * reference of chunks 1 .. count - 1 (synthesizer.cpp:195-200), which then
+ * run as one batch. text_ids[i] (text_counts[i] ids) are chunk i's prompt
+ * ids as the caller's prompt builder encodes them (EncodePromptText; for the
+ * chunks after the first without a reference voice, with chunk 0's text as
+ * the reference text). Batched items give bit for bit the codes of separate
+ * ovg_generate calls. codes[i] / unmasked_at[i] are [codebooks]
+ * [target_frames[i]]. Cancellation returns 2 with "cancelled". */
+int ovg_generate_chunks(ovg_handle* handle, int64_t count,
+                        const uint32_t* const* text_ids, const int64_t* text_counts,
+                        const int32_t* reference_codes, int64_t reference_frames,
+                        const int64_t* target_frames, const ovg_decoding* decoding,
+                        uint64_t seed, int (*cancelled)(void* user), void* user,
+                        int32_t* const* codes, int32_t* const* unmasked_at,
+                        char* error, size_t error_len);
 
 /* ovg_generate that also returns every executed step's logits, launched
  * eagerly instead of from the captured step graph. `logits_trace` receives
@@ -179,6 +203,17 @@ int ovg_generate_trace(ovg_handle* handle, const ovg_input* input,
                        int32_t* codes, int32_t* unmasked_at,
                        float* logits_trace, int64_t* executed, char* error,
                        size_t error_len);
+
+/* ovg_generate_batch launched eagerly, returning item i's logits at every
+ * step it executes: logits_traces[i] (may be NULL, as may logits_traces)
+ * receives [executed[i]][2 * target_frames_i][codebooks * audio_vocab_size]
+ * and executed[i] (may be NULL) the item's executed-step count. A test hook:
+ * the reference has no counterpart. */
+int ovg_generate_trace_batch(ovg_handle* handle, int64_t count,
+                             const ovg_input* inputs, const ovg_decoding* decoding,
+                             const uint64_t* seeds, int32_t* const* codes,
+                             int32_t* const* unmasked_at, float* const* logits_traces,
+                             int64_t* executed, char* error, size_t error_len);
 
 /* Per-kernel durations of one eager forward + score + select of `input`
  * (HIP events around every launch). Writes up to `capacity` entries and

@@ -108,6 +108,11 @@ EXPORTS = {
                                     _ptr, _ptr, _ptr, _err, _sz]),
     "ovg_generate_batch": (ctypes.c_int, [_ptr, _i64, _ptr, ctypes.POINTER(_Decoding),
                                           _ptr, _CANCEL_FN, _ptr, _ptr, _ptr, _err, _sz]),
+    "ovg_generate_trace_batch": (ctypes.c_int, [_ptr, _i64, _ptr, ctypes.POINTER(_Decoding),
+                                                _ptr, _ptr, _ptr, _ptr, _ptr, _err, _sz]),
+    "ovg_generate_chunks": (ctypes.c_int, [_ptr, _i64, _ptr, _ptr, _ptr, _i64, _ptr,
+                                           ctypes.POINTER(_Decoding), _u64, _CANCEL_FN, _ptr,
+                                           _ptr, _ptr, _err, _sz]),
     "ovg_generate_trace": (ctypes.c_int, [_ptr, ctypes.POINTER(_Input),
                                           ctypes.POINTER(_Decoding), _u64, _ptr, _ptr,
                                           _ptr, ctypes.POINTER(_i64), _err, _sz]),
@@ -442,6 +447,73 @@ class Generator:
                                         seed, _p(codes), _p(at), _p(trace),
                                         ctypes.byref(executed), err, len(err)), err)
         return GenerationResult(codes, at, executed.value, trace)
+
+    def generate_trace_batch(self, inputs: Sequence[ConditionalInput],
+                             decoding: DecodingConfig = DecodingConfig(),
+                             seeds: Optional[Sequence[int]] = None,
+                             trace: Optional[Sequence[bool]] = None
+                             ) -> List[GenerationResult]:
+        """generate_batch launched eagerly, also returning each item's logits
+        at every step it executes ([executed][2 F][codebooks * vocab]) for
+        the items whose `trace` flag is set (all by default)."""
+        n = len(inputs)
+        seeds = list(seeds) if seeds is not None else list(range(n))
+        trace = list(trace) if trace is not None else [True] * n
+        cs = (_Input * n)(*[i._c() for i in inputs])
+        seed_arr = (_u64 * n)(*seeds)
+        codes = [np.zeros((i.codebooks, i.target_frames), dtype=np.int32) for i in inputs]
+        ats = [np.zeros_like(c) for c in codes]
+        traces = []
+        for i, want in zip(inputs, trace):
+            steps = sum(1 for s in unmask_schedule(i.codebooks * i.target_frames,
+                                                   decoding.steps, decoding.t_shift) if s > 0)
+            traces.append(np.zeros((steps, 2 * i.target_frames, self._width()),
+                                   dtype=np.float32) if want else None)
+        code_ptrs = (_ptr * n)(*[_p(c) for c in codes])
+        at_ptrs = (_ptr * n)(*[_p(a) for a in ats])
+        trace_ptrs = (_ptr * n)(*[_p(t) if t is not None else None for t in traces])
+        executed = (_i64 * n)()
+        d = decoding._c()
+        err = _buf()
+        _check(lib().ovg_generate_trace_batch(
+            self._h, n, ctypes.cast(cs, _ptr), ctypes.byref(d), ctypes.cast(seed_arr, _ptr),
+            ctypes.cast(code_ptrs, _ptr), ctypes.cast(at_ptrs, _ptr),
+            ctypes.cast(trace_ptrs, _ptr), ctypes.cast(executed, _ptr), err, len(err)), err)
+        return [GenerationResult(c, a, executed[k], t)
+                for k, (c, a, t) in enumerate(zip(codes, ats, traces))]
+
+    def generate_chunks(self, text_ids: Sequence[Sequence[int]],
+                        target_frames: Sequence[int],
+                        decoding: DecodingConfig = DecodingConfig(), seed: int = 0,
+                        reference_codes=None,
+                        cancelled: Optional[Callable[[], bool]] = None
+                        ) -> List[GenerationResult]:
+        """The reference's chunk loop (synthesizer.cpp:179-201): chunk i is
+        ConditionalInput.build(text_ids[i], reference, target_frames[i]) with
+        one seed; without reference codes, chunk 0 runs first and its codes
+        are the reference of the rest, which run as one batch."""
+        n = len(text_ids)
+        texts = [np.ascontiguousarray(t, dtype=np.uint32) for t in text_ids]
+        counts = (_i64 * n)(*[len(t) for t in texts])
+        text_ptrs = (_ptr * n)(*[_p(t) if len(t) else None for t in texts])
+        frames = (_i64 * n)(*[int(f) for f in target_frames])
+        C = self.cfg["audio_codebooks"]
+        ref = (np.ascontiguousarray(reference_codes, dtype=np.int32)
+               if reference_codes is not None else None)
+        ref_frames = ref.shape[1] if ref is not None else 0
+        codes = [np.zeros((C, int(f)), dtype=np.int32) for f in target_frames]
+        ats = [np.zeros_like(c) for c in codes]
+        code_ptrs = (_ptr * n)(*[_p(c) for c in codes])
+        at_ptrs = (_ptr * n)(*[_p(a) for a in ats])
+        cb = _CANCEL_FN(lambda _user: int(bool(cancelled())) if cancelled else 0)
+        d = decoding._c()
+        err = _buf()
+        _check(lib().ovg_generate_chunks(
+            self._h, n, ctypes.cast(text_ptrs, _ptr), ctypes.cast(counts, _ptr),
+            _p(ref) if ref is not None else None, ref_frames, ctypes.cast(frames, _ptr),
+            ctypes.byref(d), seed, cb, None, ctypes.cast(code_ptrs, _ptr),
+            ctypes.cast(at_ptrs, _ptr), err, len(err)), err)
+        return [GenerationResult(c, a) for c, a in zip(codes, ats)]
 
     def profile(self, inp, repeats: int = 3) -> dict:
         """Per-kernel HIP-event timings of eager forward + score + select of

@@ -109,6 +109,8 @@ class Engine {
       (void)hipStreamDestroy(stream_);
   }
 
+  const ovg_config& config() const { return cfg_; }
+
   // ----------------------------------------------------------- weights
   void LoadSynthetic(std::uint64_t seed, float jitter);
   void LoadHost(const ovg_host_weights& w);
@@ -122,9 +124,12 @@ class Engine {
                int (*cancelled)(void*), void* user,
                const std::vector<std::int32_t*>& codes,
                const std::vector<std::int32_t*>& unmasked_at);
-  std::int64_t GenerateTrace(const Input& in, const ovg_decoding& d,
-                             std::uint64_t seed, std::int32_t* codes,
-                             std::int32_t* unmasked_at, float* trace);
+  void GenerateTrace(const std::vector<Input>& inputs, const ovg_decoding& d,
+                     const std::vector<std::uint64_t>& seeds,
+                     const std::vector<std::int32_t*>& codes,
+                     const std::vector<std::int32_t*>& unmasked_at,
+                     const std::vector<float*>& traces,
+                     std::vector<std::int64_t>* executed);
   void Profile(const std::vector<Input>& items, std::int64_t repeats,
                std::map<std::string, KernelStat>* stats);
 
@@ -964,40 +969,65 @@ int Engine::Generate(const std::vector<Input>& inputs, const ovg_decoding& d,
   return status;
 }
 
-std::int64_t Engine::GenerateTrace(const Input& in, const ovg_decoding& d,
-                                   std::uint64_t seed, std::int32_t* codes,
-                                   std::int32_t* unmasked_at, float* trace) {
-  const Layout L = Plan({in});
+// Generate launched eagerly, downloading every item's logits at each step
+// the item executes (its schedule's count is positive there).
+void Engine::GenerateTrace(const std::vector<Input>& inputs, const ovg_decoding& d,
+                           const std::vector<std::uint64_t>& seeds,
+                           const std::vector<std::int32_t*>& codes,
+                           const std::vector<std::int32_t*>& unmasked_at,
+                           const std::vector<float*>& traces,
+                           std::vector<std::int64_t>* executed) {
+  const Layout L = Plan(inputs);
+  Require(L.max_total <= kSelectThreads * kSelectPerThread,
+          "codebooks * target frames above 16384");
   Prepare(L);
   std::vector<int> launch_steps;
-  UploadDecodingPlan(L, d, {seed}, &launch_steps);
+  UploadDecodingPlan(L, d, seeds, &launch_steps);
   LaunchFill(codes_.get(), static_cast<int>(cfg_.audio_mask_id), L.outputs,
              stream_);
   LaunchFill(unmasked_at_.get(), -1, L.outputs, stream_);
   LaunchFill(epoch_.get(), 0, 1, stream_);
-  const std::size_t step_logits =
-      static_cast<std::size_t>(L.targets) *
-      static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
-  for (std::size_t k = 0; k < launch_steps.size(); ++k) {
+  const std::size_t C = static_cast<std::size_t>(cfg_.audio_codebooks);
+  const std::size_t width = C * static_cast<std::size_t>(cfg_.audio_vocab_size);
+  std::vector<std::vector<std::size_t>> schedules;
+  for (const ItemLayout& it : L.items)
+    schedules.push_back(UnmaskSchedule(C * static_cast<std::size_t>(it.frames),
+                                       static_cast<std::size_t>(d.steps), d.t_shift));
+  executed->assign(L.items.size(), 0);
+  for (const int step : launch_steps) {
     EnqueueForward(L, nullptr);
     EnqueueScore(L, d.guidance, nullptr);
-    if (trace != nullptr)
-      Check(hipMemcpyAsync(trace + k * step_logits, logits_.get(),
-                           step_logits * sizeof(float), hipMemcpyDeviceToHost,
-                           stream_),
-            "download logits");
+    for (std::size_t i = 0; i < L.items.size(); ++i) {
+      if (schedules[i][static_cast<std::size_t>(step)] == 0)
+        continue;
+      const ItemLayout& it = L.items[i];
+      const std::size_t rows = 2 * static_cast<std::size_t>(it.frames);
+      if (traces[i] != nullptr)
+        Check(hipMemcpyAsync(traces[i] + static_cast<std::size_t>((*executed)[i]) * rows * width,
+                             logits_.get() + static_cast<std::size_t>(it.logit_row) * width,
+                             rows * width * sizeof(float), hipMemcpyDeviceToHost, stream_),
+              "download logits");
+      ++(*executed)[i];
+    }
     EnqueueSelect(L, d, true, SelectStep{}, nullptr);
   }
-  const std::size_t n = static_cast<std::size_t>(L.outputs);
-  Check(hipMemcpyAsync(codes, codes_.get(), n * sizeof(std::int32_t),
+  std::vector<std::int32_t> host_codes(static_cast<std::size_t>(L.outputs));
+  std::vector<std::int32_t> host_at(static_cast<std::size_t>(L.outputs));
+  Check(hipMemcpyAsync(host_codes.data(), codes_.get(),
+                       host_codes.size() * sizeof(std::int32_t),
                        hipMemcpyDeviceToHost, stream_),
         "download codes");
-  Check(hipMemcpyAsync(unmasked_at, unmasked_at_.get(),
-                       n * sizeof(std::int32_t), hipMemcpyDeviceToHost,
+  Check(hipMemcpyAsync(host_at.data(), unmasked_at_.get(),
+                       host_at.size() * sizeof(std::int32_t), hipMemcpyDeviceToHost,
                        stream_),
         "download unmask steps");
   Check(hipStreamSynchronize(stream_), "generation");
-  return static_cast<std::int64_t>(launch_steps.size());
+  for (std::size_t i = 0; i < L.items.size(); ++i) {
+    const std::size_t n = C * static_cast<std::size_t>(L.items[i].frames);
+    std::memcpy(codes[i], host_codes.data() + L.items[i].out_base, n * sizeof(std::int32_t));
+    std::memcpy(unmasked_at[i], host_at.data() + L.items[i].out_base,
+                n * sizeof(std::int32_t));
+  }
 }
 
 void Engine::Profile(const std::vector<Input>& items, std::int64_t repeats,
@@ -1199,19 +1229,114 @@ int ovg_generate_batch(ovg_handle* handle, int64_t count,
   return status;
 }
 
+int ovg_generate_chunks(ovg_handle* handle, int64_t count,
+                        const uint32_t* const* text_ids, const int64_t* text_counts,
+                        const int32_t* reference_codes, int64_t reference_frames,
+                        const int64_t* target_frames, const ovg_decoding* decoding,
+                        uint64_t seed, int (*cancelled)(void* user), void* user,
+                        int32_t* const* codes, int32_t* const* unmasked_at, char* error,
+                        size_t error_len) {
+  const int status = Guard("OmniVoice generation: ", error, error_len, [&] {
+    ovg::Require(handle != nullptr && text_ids != nullptr && text_counts != nullptr &&
+                     target_frames != nullptr && decoding != nullptr && codes != nullptr &&
+                     unmasked_at != nullptr && count > 0,
+                 "null argument");
+    ovg::Require(reference_frames >= 0 && (reference_frames == 0 || reference_codes != nullptr),
+                 "missing reference codes");
+    const ovg_config& c = handle->engine->config();
+    const std::size_t C = static_cast<std::size_t>(c.audio_codebooks);
+    for (int64_t i = 0; i < count; ++i)
+      ovg::Require(text_counts[i] >= 0 && (text_counts[i] == 0 || text_ids[i] != nullptr) &&
+                       target_frames[i] >= 1 && codes[i] != nullptr &&
+                       unmasked_at[i] != nullptr,
+                   "bad chunk");
+    // ConditionalInput::Build (decoding.cpp:42-62) of chunk i against a
+    // reference.
+    auto build = [&](int64_t i, const std::vector<std::int32_t>& ref, std::size_t ref_frames) {
+      const std::vector<std::uint32_t> text(text_ids[i], text_ids[i] + text_counts[i]);
+      return ovg::BuildInput(text, ref, ref_frames, static_cast<std::size_t>(target_frames[i]),
+                             C, c.audio_mask_id);
+    };
+    auto input = [&](int64_t i, const std::vector<std::int32_t>& ids, std::size_t ref_frames) {
+      return ovg::Input{c.audio_codebooks,
+                        text_counts[i] + static_cast<std::int64_t>(ref_frames) + target_frames[i],
+                        text_counts[i], target_frames[i], ids.data()};
+    };
+    std::vector<std::int32_t> reference;
+    if (reference_frames > 0)
+      reference.assign(reference_codes, reference_codes + C * reference_frames);
+    std::size_t ref_frames = static_cast<std::size_t>(reference_frames);
+    int64_t first = 0;
+    if (reference_frames == 0 && count > 1) {
+      // Without a reference voice, chunk 0 runs alone and its codes carry
+      // the voice into the others (synthesizer.cpp:195-200).
+      const auto ids = build(0, {}, 0);
+      const int done = handle->engine->Generate({input(0, ids, 0)}, *decoding, {seed}, cancelled,
+                                                user, {codes[0]}, {unmasked_at[0]});
+      if (done != OVG_OK)
+        return done;
+      reference.assign(codes[0], codes[0] + C * target_frames[0]);
+      ref_frames = static_cast<std::size_t>(target_frames[0]);
+      first = 1;
+    }
+    std::vector<std::vector<std::int32_t>> ids;
+    for (int64_t i = first; i < count; ++i)
+      ids.push_back(build(i, reference, ref_frames));
+    std::vector<ovg::Input> list;
+    std::vector<std::int32_t*> code_list, at_list;
+    for (int64_t i = first; i < count; ++i) {
+      list.push_back(input(i, ids[static_cast<std::size_t>(i - first)], ref_frames));
+      code_list.push_back(codes[i]);
+      at_list.push_back(unmasked_at[i]);
+    }
+    // Every chunk takes the request's seed, as each of the reference's
+    // Generate calls does (synthesizer.cpp:70-71).
+    return handle->engine->Generate(list, *decoding,
+                                    std::vector<std::uint64_t>(list.size(), seed), cancelled,
+                                    user, code_list, at_list);
+  });
+  if (status == OVG_CANCELLED)
+    SetError(error, error_len, "cancelled");
+  return status;
+}
+
 int ovg_generate_trace(ovg_handle* handle, const ovg_input* input,
                        const ovg_decoding* decoding, uint64_t seed,
                        int32_t* codes, int32_t* unmasked_at,
                        float* logits_trace, int64_t* executed, char* error,
                        size_t error_len) {
+  return ovg_generate_trace_batch(handle, 1, input, decoding, &seed, &codes, &unmasked_at,
+                                  &logits_trace, executed, error, error_len);
+}
+
+int ovg_generate_trace_batch(ovg_handle* handle, int64_t count, const ovg_input* inputs,
+                             const ovg_decoding* decoding, const uint64_t* seeds,
+                             int32_t* const* codes, int32_t* const* unmasked_at,
+                             float* const* logits_traces, int64_t* executed,
+                             char* error, size_t error_len) {
   return Guard("OmniVoice generation: ", error, error_len, [&] {
-    ovg::Require(handle != nullptr && decoding != nullptr &&
-                     codes != nullptr && unmasked_at != nullptr,
+    ovg::Require(handle != nullptr && inputs != nullptr && decoding != nullptr &&
+                     seeds != nullptr && codes != nullptr && unmasked_at != nullptr &&
+                     count > 0,
                  "null argument");
-    const std::int64_t n = handle->engine->GenerateTrace(
-        ToInput(input), *decoding, seed, codes, unmasked_at, logits_trace);
+    std::vector<ovg::Input> list;
+    std::vector<std::uint64_t> seed_list;
+    std::vector<std::int32_t*> code_list, at_list;
+    std::vector<float*> trace_list;
+    for (int64_t i = 0; i < count; ++i) {
+      list.push_back(ToInput(&inputs[i]));
+      seed_list.push_back(seeds[i]);
+      ovg::Require(codes[i] != nullptr && unmasked_at[i] != nullptr, "null output");
+      code_list.push_back(codes[i]);
+      at_list.push_back(unmasked_at[i]);
+      trace_list.push_back(logits_traces == nullptr ? nullptr : logits_traces[i]);
+    }
+    std::vector<std::int64_t> steps;
+    handle->engine->GenerateTrace(list, *decoding, seed_list, code_list, at_list, trace_list,
+                                  &steps);
     if (executed != nullptr)
-      *executed = n;
+      for (int64_t i = 0; i < count; ++i)
+        executed[i] = steps[static_cast<std::size_t>(i)];
     return OVG_OK;
   });
 }

@@ -106,8 +106,8 @@ std::unique_ptr<Generator> Generator::LoadSynthetic(const Config& config,
   const ovg_config c = ToC(config);
   char message[kMessage] = {};
   auto state = std::make_unique<State>();
-  if (!Report(ovg_create(&c, nullptr, weight_seed, &state->handle, message,
-                         kMessage),
+  if (!Report(ovg_create_synthetic(&c, weight_seed, 0.0F, &state->handle, message,
+                                   kMessage),
               message, error))
     return nullptr;
   state->codebooks = config.audio_codebooks;

@@ -42,6 +42,12 @@
 // M-fastest, so the groups sharing a weight tile share an L2.
 #include "kernels.hpp"
 
+// No floating-point contraction in this file: every fused multiply-add in
+// the epilogues is written out, so that each tile shape (each template
+// instantiation) rounds a row's values identically and a row's result does
+// not depend on the tile height the packed row count selects.
+#pragma clang fp contract(off)
+
 namespace ovg {
 namespace {
 
@@ -212,9 +218,9 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p,
       float squares = o.v[0][e] * o.v[0][e];
 #pragma unroll
       for (int c = 1; c < 4; ++c)
-        squares += o.v[c][e] * o.v[c][e];
+        squares = __builtin_fmaf(o.v[c][e], o.v[c][e], squares);
       squares = HalfWaveSum(squares);
-      const float scale = rsqrtf(squares * (1.0F / 128.0F) + p.eps);
+      const float scale = rsqrtf(__builtin_fmaf(squares, 1.0F / 128.0F, p.eps));
       if (m >= p.m)
         continue;
       half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
@@ -222,9 +228,9 @@ __device__ __forceinline__ void QkvOwned(const GemmParams& p,
       for (int c = 0; c < 2; ++c) {
         const float a = w[c] * (o.v[c][e] * scale);
         const float b = w[c + 2] * (o.v[c + 2][e] * scale);
-        out[32 * c + j] = static_cast<half_t>(a * cs[e][c].x - b * cs[e][c].y);
+        out[32 * c + j] = static_cast<half_t>(__builtin_fmaf(a, cs[e][c].x, -(b * cs[e][c].y)));
         out[32 * c + j + 64] =
-            static_cast<half_t>(b * cs[e][c].x + a * cs[e][c].y);
+            static_cast<half_t>(__builtin_fmaf(b, cs[e][c].x, a * cs[e][c].y));
       }
     }
     return;

@@ -292,6 +292,21 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
                   int64_t in, int64_t out, int accumulate, void* stream,
                   char* error, size_t error_len);
 
+/* ovg_op_linear without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc). The split-K partials of
+ * small-M shapes live in a static device array of
+ * OVG_LINEAR_NOALLOC_SCRATCH_FLOATS floats (4 MiB per GPU, held until the
+ * process ends), which every shape ovg_op_linear accepts fits; a plan that
+ * did not would be rejected with an error. Same kernels and plan as
+ * ovg_op_linear, so the same result bit for bit; enqueued on `stream`
+ * without waiting for it. Calls that overlap on one GPU (two streams or two
+ * threads) share the array and race: serialise them. */
+#define OVG_LINEAR_NOALLOC_SCRATCH_FLOATS 1048576
+int ovg_op_linear_noalloc(const void* x, const void* w, float* y, int64_t rows,
+                          int64_t in, int64_t out, int accumulate, void* stream,
+                          char* error, size_t error_len);
+
 /* kernels::RmsNorm (reference: generator_kernels.hpp:25-28): output =
  * half(weight * x * rsqrt(mean(x^2) + eps)) per row. */
 int ovg_op_rmsnorm(const float* input, const float* weight, void* output,

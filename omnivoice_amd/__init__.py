@@ -130,6 +130,8 @@ EXPORTS = {
                                      ctypes.c_int32, _f32, _f32, _u32, _ptr, _err, _sz]),
     "ovg_op_linear": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, ctypes.c_int,
                                      _ptr, _err, _sz]),
+    "ovg_op_linear_noalloc": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64,
+                                             ctypes.c_int, _ptr, _err, _sz]),
     "ovg_op_rmsnorm": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _f32, _ptr, _err,
                                       _sz]),
     "ovg_op_attention": (ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i64, _ptr, _i64,
@@ -575,6 +577,17 @@ def op_linear(x, w, y, accumulate: bool = False, stream=None) -> None:
     err = _buf()
     _check(lib().ovg_op_linear(_dev(x), _dev(w), _dev(y), rows, k, n,
                                int(accumulate), _stream(stream), err, len(err)), err)
+
+
+def op_linear_noalloc(x, w, y, accumulate: bool = False, stream=None) -> None:
+    """op_linear without device allocation (a static split-K scratch); returns
+    without waiting for the stream."""
+    rows, k = x.shape
+    n = w.shape[0]
+    err = _buf()
+    _check(lib().ovg_op_linear_noalloc(_dev(x), _dev(w), _dev(y), rows, k, n,
+                                       int(accumulate), _stream(stream), err, len(err)),
+           err)
 
 
 def op_rmsnorm(x, weight, out, eps: float, stream=None) -> None:

@@ -421,9 +421,10 @@ void CodecEngine::Profile(std::int64_t frames, std::int64_t repeats,
   std::vector<std::int32_t> codes(static_cast<std::size_t>(cfg_.codebooks * frames));
   for (std::size_t i = 0; i < codes.size(); ++i)
     codes[i] = static_cast<std::int32_t>((i * 2654435761U) % cfg_.codebook_size);
-  Check(hipMemcpy(codes_.get(), codes.data(), codes.size() * sizeof(std::int32_t),
-                  hipMemcpyHostToDevice),
+  Check(hipMemcpyAsync(codes_.get(), codes.data(), codes.size() * sizeof(std::int32_t),
+                       hipMemcpyHostToDevice, stream_),
         "upload codes");
+  Check(hipStreamSynchronize(stream_), "upload codes");
   for (std::int64_t r = 0; r < std::max<std::int64_t>(repeats, 1); ++r) {
     Profiler prof(stream_);
     Enqueue(codes_.get(), frames, audio_.get(), stream_, &prof);

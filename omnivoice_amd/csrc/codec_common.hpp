@@ -59,11 +59,15 @@ class Source {
   const SafetensorsFile* file_;
 };
 
+// A synchronous copy from pageable memory may return before its data has
+// landed, and kernels on a non-blocking stream do not wait for it: wait for
+// the device before the buffer is used.
 template <typename T>
 void Upload(DeviceBuffer<T>& buffer, const std::vector<T>& host) {
   buffer.Reserve(host.size());
   Check(hipMemcpy(buffer.get(), host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice),
         "upload codec weights");
+  Check(hipDeviceSynchronize(), "upload codec weights");
 }
 
 // Conv1d weights [out][in][kernel] -> [kernel][in][out]. With kernel 1 and

@@ -24,7 +24,9 @@ class DeviceBuffer {
   DeviceBuffer& operator=(const DeviceBuffer&) = delete;
 
   // Grows to `count` elements (contents are lost, new memory is zeroed);
-  // returns true when it reallocated.
+  // returns true when it reallocated. The zeroing runs on the null stream,
+  // which work on a non-blocking stream does not wait for, so it is waited
+  // for here: otherwise it could land after that work's first writes.
   bool Reserve(std::size_t count) {
     if (count <= count_)
       return false;
@@ -34,6 +36,7 @@ class DeviceBuffer {
           "hipMalloc");
     Check(hipMemset(data_, 0, std::max<std::size_t>(count, 1) * sizeof(T)),
           "hipMemset");
+    Check(hipDeviceSynchronize(), "hipMemset");
     count_ = count;
     return true;
   }

@@ -962,8 +962,10 @@ void EncoderEngine::Profile(int64_t length, int64_t repeats,
   for (int64_t i = 0; i < length; ++i)
     audio[i] = 0.2F * std::sin(0.05F * static_cast<float>(i)) *
                (0.5F + 0.5F * std::sin(static_cast<float>(i) / 700.0F));
-  Check(hipMemcpy(samples_.get(), audio.data(), sizeof(float) * length, hipMemcpyHostToDevice),
+  Check(hipMemcpyAsync(samples_.get(), audio.data(), sizeof(float) * length,
+                       hipMemcpyHostToDevice, stream_),
         "upload audio");
+  Check(hipStreamSynchronize(stream_), "upload audio");
   Enqueue(samples_.get(), plan, codes_.get(), stream_, nullptr);  // warm-up
   Profiler prof(stream_);
   for (int64_t r = 0; r < repeats; ++r)

@@ -121,6 +121,33 @@ struct GemmPlan {
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue, bool split_small = false);
 void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
                 hipStream_t stream);
+// Split count of the partial-slice epilogue: a function of K steps alone.
+int PartialSplits(int k_steps);
+
+// ---------------------------------------------------------------- packed GEMM
+// The generator's projections with W packed at load into matrix-core
+// fragment order (packed_gemm.hip). GemmParams::w is then the packed matrix
+// and ldb is unused.
+enum class PackMap : int {
+  kIdentity = 0,  // block column i = output column i
+  kRope = 1,      // 128-column heads: block w holds head columns 16 w .. +15
+                  // and 64 + 16 w .. +15 (rotate-half pairs in one lane)
+  kSwiGlu = 2,    // block b holds gate rows 16 b .. +15 then up rows 16 b .. +15
+};
+// Halves a packed copy of a [rows][k] matrix takes (rows padded to 128).
+std::size_t PackedWeightHalves(int rows, int k);
+// Packs row-major fp16 w [rows][k] (for kSwiGlu: gate w and up w2, [rows][k]
+// each, packed as 2 rows outputs) on the device.
+void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map,
+                 half_t* out, hipStream_t stream);
+struct PackedPlan {
+  int xb = 4;      // tile height in 32-row blocks
+  int splits = 1;  // K split (partial-slice epilogue only)
+  int tiles = 0;   // row tiles x column tiles
+};
+PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue);
+void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue,
+                  hipStream_t stream);
 
 // ---------------------------------------------------------------- rows
 struct EmbedParams {

@@ -158,6 +158,47 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
   });
 }
 
+int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
+                         int64_t in, int64_t out, int accumulate, int64_t tile_rows,
+                         void* stream, char* error, size_t error_len) {
+  return Guard("linear: ", error, error_len, [&] {
+    ovg::Require(x && w && y, "null pointer");
+    ovg::Require(rows >= 1 && in >= 64 && out >= 1 && FitsInt(rows) &&
+                     FitsInt(in) && FitsInt(out),
+                 "empty or oversized shape");
+    ovg::Require(tile_rows == 0 || tile_rows == 32 || tile_rows == 64 || tile_rows == 96 ||
+                     tile_rows == 128,
+                 "tile rows must be 0 (planned), 32, 64, 96 or 128");
+    auto s = static_cast<hipStream_t>(stream);
+    const auto epi =
+        accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;
+    Scratch<ovg::half_t> packed(ovg::PackedWeightHalves(static_cast<int>(out),
+                                                        static_cast<int>(in)));
+    ovg::PackWeights(static_cast<const ovg::half_t*>(w), nullptr, static_cast<int>(out),
+                     static_cast<int>(in), ovg::PackMap::kIdentity, packed.data, s);
+    ovg::PackedPlan plan = ovg::PlanPacked(static_cast<int>(rows), static_cast<int>(out),
+                                           static_cast<int>(in), epi);
+    if (tile_rows != 0) {
+      plan.xb = static_cast<int>(tile_rows / 32);
+      plan.tiles = (static_cast<int>(rows) + static_cast<int>(tile_rows) - 1) /
+                   static_cast<int>(tile_rows) * ((static_cast<int>(out) + 127) / 128);
+    }
+    ovg::GemmParams p{};
+    p.x = static_cast<const ovg::half_t*>(x);
+    p.w = packed.data;
+    p.lda = static_cast<int>(in);
+    p.ldb = static_cast<int>(in);
+    p.m = static_cast<int>(rows);
+    p.n = static_cast<int>(out);
+    p.k = static_cast<int>(in);
+    p.splits = plan.splits;
+    p.y = y;
+    p.ldc = static_cast<int>(out);
+    ovg::LaunchPacked(p, plan, epi, s);
+    ovg::Check(hipStreamSynchronize(s), "linear");
+  });
+}
+
 int ovg_op_rmsnorm(const float* input, const float* weight, void* output,
                    int64_t rows, int64_t width, float epsilon, void* stream,
                    char* error, size_t error_len) {

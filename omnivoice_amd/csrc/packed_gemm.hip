@@ -1,0 +1,508 @@
+// fp16 x fp16 -> fp32 GEMM of the generator's projections on gfx950 matrix
+// cores, with the weights packed at load into matrix-core fragment order
+// (replaces the hipBLASLt calls of the reference's HalfGemm::Linear,
+// gemm.cpp:248-262, and the QkNormRope / SwiGlu kernels that followed them,
+// kernels/generator_kernels.hip:102-159, 191-200).
+//
+// Y[m][n] = sum_k X[m][k] W[n][k]. A work-group of four waves computes a
+// (32 XB) x 128 output tile; wave w owns the 32 output columns
+// 32 w .. 32 w + 31 of the tile over the whole K range, so its accumulators
+// are final when the K loop ends (no exchange between waves).
+//
+// Operands:
+//  * W (static) is packed at load (PackWeights) so that the fragment a wave
+//    needs for one 16-wide K substep of one 32-column block is 1 KB of
+//    consecutive bytes, lane l's 16 bytes at 16 l. Each wave streams its own
+//    columns global -> registers, several K steps ahead; weights never pass
+//    through LDS.
+//  * X (the activations, shared by the four waves) goes global -> registers
+//    -> LDS (a ring of four K steps, written two steps ahead, with an XOR
+//    swizzle of the 16-byte chunks so that the fragment reads are
+//    conflict-free) -> registers one step ahead, so a step's MFMAs never
+//    wait for LDS.
+// Every load is an ordinary load, so the compiler's wait counts are exact.
+//
+// The matrix-core instruction is v_mfma_f32_32x32x16_f16 (lane l receives
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] in element r). For the q/k/v and
+// SwiGLU epilogues W is its first operand: a lane holds one output row
+// (m = l % 32 of the 32-row block) and 16 of the block's 32 columns, four
+// consecutive ones per group r / 4, so column pairs meet in one lane and
+// the fp16 stores are 8-byte vectors. For the fp32 outputs X is the first
+// operand: a lane holds one column and 16 rows, and the 32 lanes of a store
+// write 128 consecutive bytes of a row (whole lines, which the write-through
+// slices need). Inside a K step, lane half h supplies K elements
+// 32 h + 8 j .. + 7 in substep j, for both operands.
+//
+// Column order inside a packed 32-column block (PackMap):
+//  * identity: block column i is output column i (o, down, audio heads);
+//  * rope: block w of a 128-column head holds head columns 16 w .. 16 w + 15
+//    and 64 + 16 w .. 64 + 16 w + 15, so both halves of a rotate-half pair
+//    are in one lane (elements r and r + 8);
+//  * swiglu: block b holds gate rows 16 b .. 16 b + 15, then the matching up
+//    rows, so gate and up of one output are in one lane (elements r, r + 8).
+//
+// Epilogues (the same Epilogue values as gemm.hip):
+//  * kStore / kAccumulate / kPartial: fp32 stores, a row's 32 columns per
+//    instruction (kPartial: write-through, each split its own slice, summed
+//    by the next row kernel);
+//  * kQkvRope: per-head RMSNorm (the squares of the wave's 32 columns, then
+//    the four waves' sums through LDS in the fixed order (0 + 1) + (2 + 3)),
+//    rotary in registers, fp16 q/k; value heads as V^T columns;
+//  * kSwiGlu: silu(gate) * up in registers, fp16.
+//
+// No floating-point contraction in this file: every fused multiply-add is
+// written out, so that the tile heights (template instantiations) round a
+// row's values identically.
+
+#include "kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ovg {
+namespace {
+
+constexpr int kXcds = 8;
+constexpr int kCus = 256;
+
+template <int XB>
+struct Packed {
+  static constexpr int kBM = 32 * XB;            // tile rows
+  static constexpr int kStageBytes = kBM * 128;  // kBM rows x 64 halves
+  static constexpr int kLds = 4 * kStageBytes;   // ring of four K steps
+};
+
+// 16-byte chunk c of LDS row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1);
+// its own inverse.
+__device__ __forceinline__ int Swizzle(int row, int chunk) {
+  return chunk ^ (row & 7) ^ ((row >> 3) & 1);
+}
+
+// Work-group barrier that first waits for this wave's LDS accesses only:
+// the W and X prefetches stay in flight across it (a fence, or the
+// compiler's barrier, would wait for every load).
+__device__ __forceinline__ void Barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
+// Keeps the compiler from moving memory operations across this point.
+__device__ __forceinline__ void AsmFence() { asm volatile("" : : : "memory"); }
+
+template <int XB, Epilogue EPI>
+__global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_m,
+                                                        int k_steps) {
+  using S = Packed<XB>;
+  extern __shared__ __align__(16) unsigned char lds[];
+  // Lane = output row (W as the first MFMA operand) for the epilogues that
+  // pair columns inside a lane; lane = output column otherwise, so that the
+  // 32 lanes of a fp32 store write 128 consecutive bytes of one row.
+  constexpr bool kRowLanes = EPI == Epilogue::kQkvRope || EPI == Epilogue::kSwiGlu;
+
+  // XCD-aware order: each XCD receives a contiguous run of tiles, rows
+  // fastest, so the row tiles that share a column block of W share an L2.
+  const int groups = gridDim.x;
+  const int pid = blockIdx.x;
+  const int xcd = pid % kXcds;
+  const int per = groups / kXcds;
+  const int extra = groups % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + pid / kXcds;
+  const int tile_m = logical % tiles_m;
+  const int rest = logical / tiles_m;
+  const int split = rest % p.splits;
+  const int tile_n = rest / p.splits;
+  // The grid is tiles_m x tiles_n x splits work-groups; nothing past it.
+  if (tile_n * 128 >= p.n)
+    return;
+  const int m0 = tile_m * S::kBM;
+  const int steps = k_steps / p.splits;  // K steps of this split
+  const int t0 = split * steps;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int block = tile_n * 4 + wave;  // this wave's packed 32-column block
+
+  // X: wave w brings rows 8 (XB w + i) + lane / 8 of every K step (8 lanes
+  // per 128-byte row), chunk lane % 8, to LDS position Swizzle(row, lane % 8).
+  // Rows past M read row M - 1 (their results are never stored).
+  const half8* x_src[XB];
+  int x_dst[XB];
+#pragma unroll
+  for (int i = 0; i < XB; ++i) {
+    const int row = 8 * (XB * wave + i) + (lane >> 3);
+    x_src[i] = reinterpret_cast<const half8*>(
+        p.x + static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda + t0 * 64) + (lane & 7);
+    x_dst[i] = row * 128 + Swizzle(row, lane & 7) * 16;
+  }
+  // W: fragment (t, j) of this block is 64 half8 at ((block k_steps + t) 4 + j) 64.
+  const half8* w_src =
+      reinterpret_cast<const half8*>(p.w) + (static_cast<size_t>(block) * k_steps + t0) * 256 + lane;
+  // Fragment reads of X: row 32 b + lane % 32, chunk 4 (lane / 32) + j.
+  int x_read[XB][4];
+#pragma unroll
+  for (int b = 0; b < XB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 32 * b + (lane & 31);
+      x_read[b][j] = row * 128 + Swizzle(row, 4 * (lane >> 5) + j) * 16;
+    }
+
+  floatx16 acc[XB];
+#pragma unroll
+  for (int b = 0; b < XB; ++b)
+    acc[b] = floatx16{};
+
+  half8 wf[4][4];       // W of steps t .. t + 3, slot t % 4
+  half8 xs[2][XB];      // X of steps t + 2 and t + 3, slot t % 2
+  half8 fr[2][4][XB];   // fragments of X(t) (slot t % 2) and X(t + 1)
+  auto load_w = [&](half8 (&dst)[4], int t) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dst[j] = w_src[(t * 4 + j) * 64];
+  };
+  auto load_x = [&](half8 (&dst)[XB], int t) {
+#pragma unroll
+    for (int i = 0; i < XB; ++i)
+      dst[i] = x_src[i][t * 8];  // 64 halves = 8 half8 per K step
+  };
+  auto store_x = [&](const half8 (&src)[XB], int buf) {
+#pragma unroll
+    for (int i = 0; i < XB; ++i)
+      *reinterpret_cast<half8*>(lds + buf * S::kStageBytes + x_dst[i]) = src[i];
+  };
+  auto read_frag = [&](half8 (&dst)[XB], int buf, int j) {
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+      dst[b] = *reinterpret_cast<const half8*>(lds + buf * S::kStageBytes + x_read[b][j]);
+  };
+
+  // Prologue: W of steps 0 .. 3 and X of steps 0 .. 3 are loaded; X(0) and
+  // X(1) go to LDS buffers 0 and 1, X(0)'s fragments to registers. Step
+  // indices past the last are clamped to it (in-bounds reloads whose values
+  // are never used), so that no load sits under a condition: a conditional
+  // load makes the compiler's wait counts assume it was skipped and wait for
+  // the loads before it.
+  const int last = steps - 1;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    load_w(wf[s], min(s, last));
+  {
+    half8 x0[XB], x1[XB];
+    load_x(x0, 0);
+    load_x(x1, min(1, last));
+    load_x(xs[0], min(2, last));
+    load_x(xs[1], min(3, last));
+    store_x(x0, 0);
+    store_x(x1, 1);
+  }
+  Barrier();
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    read_frag(fr[0][j], 0, j);
+
+  // Step t (LDS buffers by t % 4, register slots by t % 4 and t % 2): write
+  // X(t + 2) into buffer (t + 2) % 4 (its previous content, X(t - 2), was
+  // last read in step t - 3) and reload those registers with X(t + 4); run
+  // the 16 MFMAs of step t from fragments already in registers while reading
+  // X(t + 1)'s fragments from buffer (t + 1) % 4 (written in step t - 1,
+  // before the barrier that ended it), so no MFMA waits for LDS; reload W's
+  // slot with W(t + 4); end at a barrier that first waits for all of the
+  // step's LDS operations, after which X(t + 2) is readable. (Letting the
+  // fragment reads run on across the barrier measured no faster.)
+  auto step = [&](int t, auto slot) {
+    constexpr int ws = decltype(slot)::value;  // t % 4
+    constexpr int xo = ws & 1;                 // t % 2
+    store_x(xs[xo], (ws + 2) & 3);
+    AsmFence();
+    load_x(xs[xo], min(t + 4, last));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      read_frag(fr[1 - xo][j], (ws + 1) & 3, j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < XB; ++b)
+        acc[b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[b])
+                           : Mfma32(fr[xo][j][b], wf[ws][j], acc[b]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_w(wf[ws], min(t + 4, last));
+    Barrier();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  const int whole = steps & ~3;
+  for (int t = 0; t < whole; t += 4) {
+    step(t, I0{});
+    step(t + 1, I1{});
+    step(t + 2, I2{});
+    step(t + 3, I3{});
+  }
+  // The last steps % 4 steps (only shapes whose K range per split is not a
+  // multiple of 256).
+  if (whole < steps)
+    step(whole, I0{});
+  if (whole + 1 < steps)
+    step(whole + 1, I1{});
+  if (whole + 2 < steps)
+    step(whole + 2, I2{});
+
+  // ------------------------------------------------------------- epilogue
+  const int h = lane >> 5;
+  const int col = lane & 31;
+  if constexpr (EPI == Epilogue::kStore || EPI == Epilogue::kAccumulate ||
+                EPI == Epilogue::kPartial) {
+    // Lane = column 32 wave + lane % 32 of the tile; element r of X block b
+    // is row 32 b + 8 (r / 4) + 4 (lane / 32) + r % 4.
+    float* y = p.y + (EPI == Epilogue::kPartial ? static_cast<size_t>(split) * p.split_stride : 0);
+    const int n = tile_n * 128 + 32 * wave + col;
+    if (n < p.n) {
+#pragma unroll
+      for (int b = 0; b < XB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m >= p.m)
+            continue;
+          float* dst = y + static_cast<size_t>(m) * p.ldc + n;
+          if constexpr (EPI == Epilogue::kAccumulate)
+            *dst = *dst + acc[b][r];
+          else if constexpr (EPI == Epilogue::kPartial)
+            StoreThrough(dst, acc[b][r]);
+          else
+            *dst = acc[b][r];
+        }
+    }
+  } else if constexpr (EPI == Epilogue::kSwiGlu) {
+    // Block `block` holds gate and up of outputs 16 block .. 16 block + 15.
+    const int a_base = 16 * block + 4 * h;
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      const int m = m0 + 32 * b + col;
+      if (m >= p.m)
+        continue;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        half4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gate = acc[b][4 * g + i];
+          const float up = acc[b][4 * g + 8 + i];
+          v[i] = static_cast<half_t>(gate / (1.0F + __expf(-gate)) * up);
+        }
+        *reinterpret_cast<half4*>(p.act + static_cast<size_t>(m) * p.ldh + a_base + 8 * g) = v;
+      }
+    }
+  } else if constexpr (EPI == Epilogue::kQkvRope) {
+    const int slot = tile_n;  // one 128-column head per tile
+    if (slot < p.heads + p.kv_heads) {
+      // Sum of squares of the wave's 32 columns of each row, then of the
+      // four waves in a fixed order.
+      float* sums = reinterpret_cast<float*>(lds);  // [4][kBM]
+      float part[XB];
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        float s = acc[b][0] * acc[b][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r)
+          s = __builtin_fmaf(acc[b][r], acc[b][r], s);
+        part[b] = s + __shfl_xor(s, 32);
+      }
+      // The K loop's last barrier separates the LDS reads of X from these
+      // writes.
+      if (h == 0) {
+#pragma unroll
+        for (int b = 0; b < XB; ++b)
+          sums[wave * S::kBM + 32 * b + col] = part[b];
+      }
+      __syncthreads();
+      const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
+      // This lane's rotary indices: c = 16 wave + 8 g + 4 h + i, g < 2.
+      const int c_base = 16 * wave + 4 * h;
+      float w_lo[2][4], w_hi[2][4];
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w_lo[g][i] = weight[c_base + 8 * g + i];
+          w_hi[g][i] = weight[64 + c_base + 8 * g + i];
+        }
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int r_local = 32 * b + col;
+        const int m = m0 + r_local;
+        const float total = (sums[r_local] + sums[S::kBM + r_local]) +
+                            (sums[2 * S::kBM + r_local] + sums[3 * S::kBM + r_local]);
+        const float scale = rsqrtf(__builtin_fmaf(total, 1.0F / 128.0F, p.eps));
+        if (m >= p.m)
+          continue;
+        const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
+        half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + c_base;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          half4 lo, hi;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float2 rot = cs[8 * g + i];
+            const float a = w_lo[g][i] * (acc[b][4 * g + i] * scale);
+            const float bb = w_hi[g][i] * (acc[b][4 * g + 8 + i] * scale);
+            lo[i] = static_cast<half_t>(__builtin_fmaf(a, rot.x, -(bb * rot.y)));
+            hi[i] = static_cast<half_t>(__builtin_fmaf(bb, rot.x, a * rot.y));
+          }
+          *reinterpret_cast<half4*>(out + 8 * g) = lo;
+          *reinterpret_cast<half4*>(out + 64 + 8 * g) = hi;
+        }
+      }
+    } else {
+      // Value head gv: V^T[gv][d][VtColumn(row)], d the head column of the
+      // element (rope order inside the block).
+      const int gv = slot - p.heads - p.kv_heads;
+      const int c_base = 16 * wave + 4 * h;
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int m = m0 + 32 * b + col;
+        if (m >= p.m)
+          continue;
+        const int column = VtColumn(m);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
+          p.vt[static_cast<size_t>(gv * 128 + d) * p.ldvt + column] =
+              static_cast<half_t>(acc[b][r]);
+        }
+      }
+    }
+  }
+}
+
+// Packs row-major fp16 W [rows][K] into the fragment order above: half8
+// number ((block K/64 + t) 4 + j) 64 + l holds W[row(block, l % 32)][64 t +
+// 32 (l / 32) + 8 j .. + 7]; rows past `rows` are zero. One thread per half8.
+__global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, int k,
+                                  int blocks, PackMap map, half8* out) {
+  const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
+  const size_t o = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (o >= total)
+    return;
+  const int lane = static_cast<int>(o & 63);
+  const int j = static_cast<int>((o >> 6) & 3);
+  const size_t bt = o >> 8;  // block * (k / 64) + t
+  const int t = static_cast<int>(bt % (k / 64));
+  const int block = static_cast<int>(bt / (k / 64));
+  const int i = lane & 31;
+  const half_t* src = w;
+  int row = 32 * block + i;
+  if (map == PackMap::kRope) {
+    const int head = block / 4, wv = block % 4;
+    row = 128 * head + (i < 16 ? 16 * wv + i : 64 + 16 * wv + (i - 16));
+  } else if (map == PackMap::kSwiGlu) {
+    row = 16 * block + (i & 15);
+    src = i < 16 ? w : w2;
+  }
+  half8 v = {};
+  if (row < rows)
+    v = *reinterpret_cast<const half8*>(src + static_cast<size_t>(row) * k + 64 * t +
+                                        32 * (lane >> 5) + 8 * j);
+  out[o] = v;
+}
+
+template <int XB, Epilogue EPI>
+void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  const int tiles_m = (p.m + Packed<XB>::kBM - 1) / Packed<XB>::kBM;
+  const int tiles_n = (p.n + 127) / 128;
+  const int groups = tiles_m * tiles_n * p.splits;
+  Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
+  Dispatch(PackedGemmKernel<XB, EPI>, dim3(groups), dim3(256), Packed<XB>::kLds, stream, true,
+           true, p, tiles_m, p.k / 64);
+}
+
+template <Epilogue EPI>
+void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  switch (plan.xb) {
+    case 1: LaunchPackedXB<1, EPI>(p, plan, stream); break;
+    case 2: LaunchPackedXB<2, EPI>(p, plan, stream); break;
+    case 3: LaunchPackedXB<3, EPI>(p, plan, stream); break;
+    default: LaunchPackedXB<4, EPI>(p, plan, stream); break;
+  }
+}
+
+}  // namespace
+
+std::size_t PackedWeightHalves(int rows, int k) {
+  return static_cast<std::size_t>((rows + 127) / 128 * 128) * k;
+}
+
+void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map,
+                 half_t* out, hipStream_t stream) {
+  Require(k % 64 == 0 && rows > 0, "pack: K must be a positive multiple of 64");
+  Require(map != PackMap::kSwiGlu || w2 != nullptr, "pack: SwiGLU packing needs gate and up");
+  // Blocks of 32 columns, padded to whole 128-column tiles.
+  const int out_rows = map == PackMap::kSwiGlu ? 2 * rows : rows;
+  const int blocks = (out_rows + 127) / 128 * 4;
+  const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
+  const int threads = 256;
+  PackWeightsKernel<<<static_cast<unsigned>((total + threads - 1) / threads), threads, 0,
+                      stream>>>(w, w2, rows, k, blocks, map, reinterpret_cast<half8*>(out));
+  Check(hipGetLastError(), "pack launch");
+}
+
+PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
+  PackedPlan plan;
+  const int tiles_n = (n + 127) / 128;
+  const int k_steps = k / 64;
+  plan.splits = epilogue == Epilogue::kPartial ? PartialSplits(k_steps) : 1;
+  const int steps = k_steps / plan.splits;
+  // The K loop is bound by the operands each CU pulls from L2 per K step
+  // (32 XB rows of X plus 128 columns of W: XB + 4 units of 4 KB); a tile
+  // also pays a fixed cost (first loads, epilogue) of about 50 units.
+  // Estimated time: rounds of work-groups over the CUs times that.
+  double best = 0.0;
+  for (const int xb : {4, 3, 2, 1}) {
+    const int tiles = (m + 32 * xb - 1) / (32 * xb) * tiles_n * plan.splits;
+    const int rounds = (tiles + kCus - 1) / kCus;
+    const double cost = rounds * (static_cast<double>(steps) * (xb + 4) + 50.0);
+    if (best == 0.0 || cost < best) {
+      best = cost;
+      plan.xb = xb;
+    }
+  }
+  plan.tiles = (m + 32 * plan.xb - 1) / (32 * plan.xb) * tiles_n;
+  return plan;
+}
+
+void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue,
+                  hipStream_t stream) {
+  Require(p.m > 0 && p.n > 0 && p.k > 0, "gemm: empty shape");
+  Require(p.k % 64 == 0, "gemm: K must be a multiple of 64");
+  Require(p.splits == plan.splits && (p.k / 64) % p.splits == 0,
+          "gemm: K steps not divisible by the split count");
+  Require(p.lda % 8 == 0, "gemm: the row stride of X must be a multiple of 8");
+  Require(plan.xb >= 1 && plan.xb <= 4, "gemm: tile height of 1 to 4 blocks of 32 rows");
+  switch (epilogue) {
+    case Epilogue::kStore:
+    case Epilogue::kAccumulate:
+    case Epilogue::kPartial:
+      Require(epilogue != Epilogue::kPartial ||
+                  (p.y != nullptr && p.split_stride >= static_cast<std::size_t>(p.m) * p.ldc),
+              "gemm: partial slices overlap");
+      if (epilogue == Epilogue::kStore)
+        LaunchPackedEpi<Epilogue::kStore>(p, plan, stream);
+      else if (epilogue == Epilogue::kAccumulate)
+        LaunchPackedEpi<Epilogue::kAccumulate>(p, plan, stream);
+      else
+        LaunchPackedEpi<Epilogue::kPartial>(p, plan, stream);
+      break;
+    case Epilogue::kQkvRope:
+      Require(p.n == (p.heads + 2 * p.kv_heads) * 128,
+              "gemm: q/k/v epilogue needs N = (heads + 2 kv_heads) * 128");
+      Require(p.ldvt % 16 == 0 && p.ldq % 4 == 0, "gemm: q/k/v output strides");
+      LaunchPackedEpi<Epilogue::kQkvRope>(p, plan, stream);
+      break;
+    case Epilogue::kSwiGlu:
+      Require(p.n % 128 == 0 && p.ldh % 4 == 0, "gemm: SwiGLU epilogue needs N % 128 == 0");
+      LaunchPackedEpi<Epilogue::kSwiGlu>(p, plan, stream);
+      break;
+  }
+  Check(hipGetLastError(), "gemm launch");
+}
+
+}  // namespace ovg

@@ -113,6 +113,8 @@ class Engine {
 
   // ----------------------------------------------------------- weights
   void LoadSynthetic(std::uint64_t seed, float jitter);
+  void UploadPacked(DeviceBuffer<half_t>& dst, const std::vector<half_t>& host, int rows,
+                    int k, PackMap map);
   void LoadHost(const ovg_host_weights& w);
   std::int64_t DeviceBytes() const;
 
@@ -185,7 +187,7 @@ class Engine {
   DeviceBuffer<AttentionWork> work_;
   DeviceBuffer<ScoreItem> score_items_;
   DeviceBuffer<SelectItem> select_items_;
-  DeviceBuffer<float> hidden_, logits_, conf_, noise_, partials_, part_;
+  DeviceBuffer<float> hidden_, logits_, conf_, noise_, part_;
   DeviceBuffer<half_t> normed_, qk_, vt_, attn_, act_, final_normed_;
   DeviceBuffer<int> pred_, codes_, unmasked_at_;
   DeviceBuffer<SelectStep> plan_;
@@ -220,15 +222,27 @@ void Engine::UploadRope() {
         "upload rotary table");
 }
 
-namespace {
-
-// The fused gate/up matrix interleaved per 128-row tile: tile t holds gate
-// rows [64 t, 64 t + 64) then up rows [64 t, 64 t + 64).
-std::size_t GateUpRow(std::size_t tile, bool up, std::size_t i) {
-  return tile * 128 + (up ? 64 : 0) + i;
+// Uploads a row-major fp16 matrix and packs it on the device into the
+// matrix-core fragment order of the packed GEMM (for kSwiGlu, `host` holds
+// the gate rows, then the up rows, `rows` each).
+void Engine::UploadPacked(DeviceBuffer<half_t>& dst, const std::vector<half_t>& host,
+                          int rows, int k, PackMap map) {
+  // The copy goes on the engine's stream, ahead of the packing kernel: a
+  // synchronous copy from pageable memory may return before its data has
+  // landed, and the non-blocking stream would not wait for it.
+  DeviceBuffer<half_t> staging;
+  staging.Reserve(host.size());
+  Check(hipMemcpyAsync(staging.get(), host.data(), host.size() * sizeof(half_t),
+                       hipMemcpyHostToDevice, stream_),
+        "upload weights");
+  const int out_rows = map == PackMap::kSwiGlu ? 2 * rows : rows;
+  dst.Reserve(PackedWeightHalves(out_rows, k));
+  PackWeights(staging.get(),
+              map == PackMap::kSwiGlu ? staging.get() + static_cast<std::size_t>(rows) * k
+                                      : nullptr,
+              rows, k, map, dst.get(), stream_);
+  Check(hipStreamSynchronize(stream_), "pack weights");
 }
-
-}  // namespace
 
 void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
   const std::size_t h = static_cast<std::size_t>(cfg_.hidden_size);
@@ -237,7 +251,6 @@ void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
   const std::size_t kv_rows = static_cast<std::size_t>(cfg_.kv_heads) * 128;
   const std::size_t audio_rows =
       static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
-  const std::size_t head_rows = (audio_rows + 127) / 128 * 128;
   UploadRope();
 
   // Embedding tables (fp32 holding fp16-rounded values), in slabs.
@@ -264,12 +277,10 @@ void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
           "upload audio embeddings");
   }
   {
-    std::vector<half_t> host(head_rows * h, static_cast<half_t>(0.0F));
+    std::vector<half_t> host(audio_rows * h, static_cast<half_t>(0.0F));
     SynthHalf(seed, kAudioHeadTensor, 0, audio_rows * h, host.data());
-    heads_.Reserve(host.size());
-    Check(hipMemcpy(heads_.get(), host.data(), host.size() * sizeof(half_t),
-                    hipMemcpyHostToDevice),
-          "upload audio heads");
+    UploadPacked(heads_, host, static_cast<int>(audio_rows), static_cast<int>(h),
+                 PackMap::kIdentity);
   }
   {
     std::vector<float> host(h);
@@ -281,13 +292,6 @@ void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
   }
   layers_ = std::vector<Layer>(static_cast<std::size_t>(cfg_.layers));
   std::vector<half_t> matrix;
-  std::vector<half_t> part;
-  auto upload_half = [](DeviceBuffer<half_t>& b, const std::vector<half_t>& v) {
-    b.Reserve(v.size());
-    Check(hipMemcpy(b.get(), v.data(), v.size() * sizeof(half_t),
-                    hipMemcpyHostToDevice),
-          "upload weights");
-  };
   auto upload_norm = [&](DeviceBuffer<float>& b, std::uint64_t tensor,
                          std::size_t n) {
     std::vector<float> v(n);
@@ -306,27 +310,25 @@ void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
               matrix.data() + q_rows * h);
     SynthHalf(seed, LayerTensor(l, OVG_LAYER_V_PROJ), 0, kv_rows * h,
               matrix.data() + (q_rows + kv_rows) * h);
-    upload_half(L.qkv, matrix);
+    UploadPacked(L.qkv, matrix, static_cast<int>(q_rows + 2 * kv_rows), static_cast<int>(h),
+                 PackMap::kRope);
     matrix.assign(h * q_rows, static_cast<half_t>(0.0F));
     SynthHalf(seed, LayerTensor(l, OVG_LAYER_O_PROJ), 0, h * q_rows,
               matrix.data());
-    upload_half(L.output, matrix);
-    // gate and up, interleaved per 64-row block.
+    UploadPacked(L.output, matrix, static_cast<int>(h), static_cast<int>(q_rows),
+                 PackMap::kIdentity);
+    // gate rows, then up rows.
     matrix.assign(2 * inter * h, static_cast<half_t>(0.0F));
-    part.assign(inter * h, static_cast<half_t>(0.0F));
-    for (int which = 0; which < 2; ++which) {
-      SynthHalf(seed,
-                LayerTensor(l, which == 0 ? OVG_LAYER_GATE_PROJ : OVG_LAYER_UP_PROJ),
-                0, inter * h, part.data());
-      for (std::size_t r = 0; r < inter; ++r)
-        std::memcpy(matrix.data() + GateUpRow(r / 64, which == 1, r % 64) * h,
-                    part.data() + r * h, h * sizeof(half_t));
-    }
-    upload_half(L.gate_up, matrix);
+    SynthHalf(seed, LayerTensor(l, OVG_LAYER_GATE_PROJ), 0, inter * h, matrix.data());
+    SynthHalf(seed, LayerTensor(l, OVG_LAYER_UP_PROJ), 0, inter * h,
+              matrix.data() + inter * h);
+    UploadPacked(L.gate_up, matrix, static_cast<int>(inter), static_cast<int>(h),
+                 PackMap::kSwiGlu);
     matrix.assign(h * inter, static_cast<half_t>(0.0F));
     SynthHalf(seed, LayerTensor(l, OVG_LAYER_DOWN_PROJ), 0, h * inter,
               matrix.data());
-    upload_half(L.down, matrix);
+    UploadPacked(L.down, matrix, static_cast<int>(h), static_cast<int>(inter),
+                 PackMap::kIdentity);
     upload_norm(L.input_norm, LayerTensor(l, OVG_LAYER_INPUT_NORM), h);
     upload_norm(L.post_norm, LayerTensor(l, OVG_LAYER_POST_NORM), h);
     upload_norm(L.q_norm, LayerTensor(l, OVG_LAYER_Q_NORM), 128);
@@ -345,7 +347,6 @@ void Engine::LoadHost(const ovg_host_weights& w) {
   const std::size_t kv_rows = static_cast<std::size_t>(cfg_.kv_heads) * 128;
   const std::size_t audio_rows =
       static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
-  const std::size_t head_rows = (audio_rows + 127) / 128 * 128;
   UploadRope();
   auto upload_float = [](DeviceBuffer<float>& b, const float* src,
                          std::size_t n) {
@@ -361,21 +362,15 @@ void Engine::LoadHost(const ovg_host_weights& w) {
         dst[i] = ToHalf(src[i]);
     });
   };
-  auto upload_half = [](DeviceBuffer<half_t>& b, const std::vector<half_t>& v) {
-    b.Reserve(v.size());
-    Check(hipMemcpy(b.get(), v.data(), v.size() * sizeof(half_t),
-                    hipMemcpyHostToDevice),
-          "upload weights");
-  };
   upload_float(text_, w.text_embeddings,
                static_cast<std::size_t>(cfg_.vocab_size) * h);
   upload_float(audio_, w.audio_embeddings, audio_rows * h);
   upload_float(final_norm_, w.final_norm, h);
-  std::vector<half_t> matrix(head_rows * h, static_cast<half_t>(0.0F));
+  std::vector<half_t> matrix(audio_rows * h, static_cast<half_t>(0.0F));
   to_half(w.audio_heads, audio_rows * h, matrix.data());
-  upload_half(heads_, matrix);
+  UploadPacked(heads_, matrix, static_cast<int>(audio_rows), static_cast<int>(h),
+               PackMap::kIdentity);
   layers_ = std::vector<Layer>(static_cast<std::size_t>(cfg_.layers));
-  std::vector<half_t> part;
   for (std::int64_t l = 0; l < cfg_.layers; ++l) {
     const float* const* t = w.layers + l * OVG_LAYER_TENSORS;
     Layer& L = layers_[static_cast<std::size_t>(l)];
@@ -384,23 +379,21 @@ void Engine::LoadHost(const ovg_host_weights& w) {
     to_half(t[OVG_LAYER_K_PROJ], kv_rows * h, matrix.data() + q_rows * h);
     to_half(t[OVG_LAYER_V_PROJ], kv_rows * h,
             matrix.data() + (q_rows + kv_rows) * h);
-    upload_half(L.qkv, matrix);
+    UploadPacked(L.qkv, matrix, static_cast<int>(q_rows + 2 * kv_rows), static_cast<int>(h),
+                 PackMap::kRope);
     matrix.assign(h * q_rows, static_cast<half_t>(0.0F));
     to_half(t[OVG_LAYER_O_PROJ], h * q_rows, matrix.data());
-    upload_half(L.output, matrix);
+    UploadPacked(L.output, matrix, static_cast<int>(h), static_cast<int>(q_rows),
+                 PackMap::kIdentity);
     matrix.assign(2 * inter * h, static_cast<half_t>(0.0F));
-    part.assign(inter * h, static_cast<half_t>(0.0F));
-    for (int which = 0; which < 2; ++which) {
-      to_half(t[which == 0 ? OVG_LAYER_GATE_PROJ : OVG_LAYER_UP_PROJ],
-              inter * h, part.data());
-      for (std::size_t r = 0; r < inter; ++r)
-        std::memcpy(matrix.data() + GateUpRow(r / 64, which == 1, r % 64) * h,
-                    part.data() + r * h, h * sizeof(half_t));
-    }
-    upload_half(L.gate_up, matrix);
+    to_half(t[OVG_LAYER_GATE_PROJ], inter * h, matrix.data());
+    to_half(t[OVG_LAYER_UP_PROJ], inter * h, matrix.data() + inter * h);
+    UploadPacked(L.gate_up, matrix, static_cast<int>(inter), static_cast<int>(h),
+                 PackMap::kSwiGlu);
     matrix.assign(h * inter, static_cast<half_t>(0.0F));
     to_half(t[OVG_LAYER_DOWN_PROJ], h * inter, matrix.data());
-    upload_half(L.down, matrix);
+    UploadPacked(L.down, matrix, static_cast<int>(h), static_cast<int>(inter),
+                 PackMap::kIdentity);
     upload_float(L.input_norm, t[OVG_LAYER_INPUT_NORM], h);
     upload_float(L.post_norm, t[OVG_LAYER_POST_NORM], h);
     upload_float(L.q_norm, t[OVG_LAYER_Q_NORM], 128);
@@ -420,7 +413,7 @@ std::int64_t Engine::DeviceBytes() const {
            gather_.bytes() + epoch_.bytes() + work_.bytes() +
            score_items_.bytes() + select_items_.bytes() + hidden_.bytes() +
            logits_.bytes() + conf_.bytes() + noise_.bytes() +
-           partials_.bytes() + part_.bytes() + normed_.bytes() + qk_.bytes() +
+           part_.bytes() + normed_.bytes() + qk_.bytes() +
            vt_.bytes() +
            attn_.bytes() + act_.bytes() + final_normed_.bytes() +
            pred_.bytes() + codes_.bytes() + unmasked_at_.bytes() +
@@ -564,21 +557,25 @@ void Engine::Prepare(const Layout& L) {
   Grow(conf_, static_cast<std::size_t>(L.outputs));
   Grow(codes_, static_cast<std::size_t>(L.outputs));
   Grow(unmasked_at_, static_cast<std::size_t>(L.outputs));
-  std::size_t partials = 0;
   const int M = L.rows;
   const int K = static_cast<int>(cfg_.hidden_size);
-  for (const auto& [m, n, k] : {
-           std::tuple<int, int, int>{M, static_cast<int>(qk_width + cfg_.kv_heads * 128), K},
-           {M, static_cast<int>(2 * cfg_.intermediate_size), K},
-           {L.targets, static_cast<int>(width), K}}) {
-    const GemmPlan plan = PlanGemm(m, n, k, Epilogue::kStore);
-    partials = std::max(partials, plan.partial_floats);
-  }
-  Grow(partials_, std::max<std::size_t>(partials, 1));
   const int slices = std::max(
-      PlanGemm(M, K, static_cast<int>(cfg_.heads * 128), Epilogue::kPartial).splits,
-      PlanGemm(M, K, static_cast<int>(cfg_.intermediate_size), Epilogue::kPartial).splits);
+      PlanPacked(M, K, static_cast<int>(cfg_.heads * 128), Epilogue::kPartial).splits,
+      PlanPacked(M, K, static_cast<int>(cfg_.intermediate_size), Epilogue::kPartial).splits);
   Grow(part_, static_cast<std::size_t>(slices) * ra * h);
+  // The last key tile of the last sequence reads up to 32 rows past the
+  // packed rows, which no kernel writes: keep those K rows and V^T columns
+  // zero, since a masked key's probability 0 times a non-finite stale value
+  // would still be NaN. (Rows inside the packed range, alignment padding
+  // included, are written by the q/k/v GEMM every layer.)
+  Check(hipMemsetAsync(qk_.get() + static_cast<std::size_t>(L.rows) * qk_width, 0,
+                       static_cast<std::size_t>(L.rows_alloc - L.rows) * qk_width * sizeof(half_t),
+                       stream_),
+        "clear key slack");
+  Check(hipMemset2DAsync(vt_.get() + L.rows, static_cast<std::size_t>(ldvt) * sizeof(half_t), 0,
+                         static_cast<std::size_t>(ldvt - L.rows) * sizeof(half_t),
+                         static_cast<std::size_t>(cfg_.kv_heads) * 128, stream_),
+        "clear value slack");
   auto up = [&](void* dst, const void* src, std::size_t bytes) {
     Check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_),
           "upload batch");
@@ -635,7 +632,7 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
   auto gemm = [&](const char* name, Epilogue epi, const half_t* x, int lda,
                   const half_t* w, int m, int n, int k, double real_m,
                   double out_bytes, const std::function<void(GemmParams&)>& set) {
-    const GemmPlan plan = PlanGemm(m, n, k, epi);
+    const PackedPlan plan = PlanPacked(m, n, k, epi);
     GemmParams p{};
     p.x = x;
     p.w = w;
@@ -645,11 +642,10 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     p.n = n;
     p.k = k;
     p.splits = plan.splits;
-    p.partials = partials_.get();
     set(p);
     const double flops = 2.0 * real_m * n * k;
     const double bytes = 2.0 * n * k + 2.0 * real_m * k + out_bytes;
-    Run(prof, name, flops, bytes, [&] { LaunchGemm(p, plan, epi, stream_); });
+    Run(prof, name, flops, bytes, [&] { LaunchPacked(p, plan, epi, stream_); });
   };
 
   AttentionParams ap{};
@@ -690,8 +686,8 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     Run(prof, name, 0.0, static_cast<double>(rows) * H * (4.0 * (splits + 2) + 2.0),
         [&] { LaunchAddNorm(a, stream_); });
   };
-  const int o_splits = PlanGemm(M, H, heads_width, Epilogue::kPartial).splits;
-  const int down_splits = PlanGemm(M, H, I, Epilogue::kPartial).splits;
+  const int o_splits = PlanPacked(M, H, heads_width, Epilogue::kPartial).splits;
+  const int down_splits = PlanPacked(M, H, I, Epilogue::kPartial).splits;
   for (std::size_t l = 0; l < layers_.size(); ++l) {
     const Layer& W = layers_[l];
     gemm("gemm_qkv_rope", Epilogue::kQkvRope, normed_.get(), H, W.qkv.get(),

@@ -131,7 +131,7 @@ EXPORTS = {
     "ovg_op_linear": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, ctypes.c_int,
                                      _ptr, _err, _sz]),
     "ovg_op_linear_packed": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64,
-                                            ctypes.c_int, _i64, _ptr, _err, _sz]),
+                                            ctypes.c_int, _i64, _i64, _ptr, _err, _sz]),
     "ovg_op_linear_noalloc": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64,
                                              ctypes.c_int, _ptr, _err, _sz]),
     "ovg_op_rmsnorm": (ctypes.c_int, [_ptr, _ptr, _ptr, _i64, _i64, _f32, _ptr, _err,
@@ -582,13 +582,15 @@ def op_linear(x, w, y, accumulate: bool = False, stream=None) -> None:
 
 
 def op_linear_packed(x, w, y, accumulate: bool = False, tile_rows: int = 0,
-                     stream=None) -> None:
-    """op_linear through the generator's packed-weight kernel."""
+                     tile_cols: int = 0, stream=None) -> None:
+    """op_linear through the generator's packed-weight kernel (tile forced
+    when tile_rows and tile_cols are given)."""
     rows, k = x.shape
     n = w.shape[0]
     err = _buf()
     _check(lib().ovg_op_linear_packed(_dev(x), _dev(w), _dev(y), rows, k, n, int(accumulate),
-                                      tile_rows, _stream(stream), err, len(err)), err)
+                                      tile_rows, tile_cols, _stream(stream), err, len(err)),
+           err)
 
 
 def op_linear_noalloc(x, w, y, accumulate: bool = False, stream=None) -> None:

@@ -134,7 +134,7 @@ enum class PackMap : int {
                   // and 64 + 16 w .. +15 (rotate-half pairs in one lane)
   kSwiGlu = 2,    // block b holds gate rows 16 b .. +15 then up rows 16 b .. +15
 };
-// Halves a packed copy of a [rows][k] matrix takes (rows padded to 128).
+// Halves a packed copy of a [rows][k] matrix takes (rows padded to 256).
 std::size_t PackedWeightHalves(int rows, int k);
 // Packs row-major fp16 w [rows][k] (for kSwiGlu: gate w and up w2, [rows][k]
 // each, packed as 2 rows outputs) on the device.
@@ -142,6 +142,7 @@ void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map
                  half_t* out, hipStream_t stream);
 struct PackedPlan {
   int xb = 4;      // tile height in 32-row blocks
+  int wb = 1;      // tile width in 128-column units (2: the 128 x 256 tile)
   int splits = 1;  // K split (partial-slice epilogue only)
   int tiles = 0;   // row tiles x column tiles
 };

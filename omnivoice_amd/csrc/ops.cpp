@@ -160,7 +160,7 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
 
 int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
                          int64_t in, int64_t out, int accumulate, int64_t tile_rows,
-                         void* stream, char* error, size_t error_len) {
+                         int64_t tile_cols, void* stream, char* error, size_t error_len) {
   return Guard("linear: ", error, error_len, [&] {
     ovg::Require(x && w && y, "null pointer");
     ovg::Require(rows >= 1 && in >= 64 && out >= 1 && FitsInt(rows) &&
@@ -169,6 +169,9 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
     ovg::Require(tile_rows == 0 || tile_rows == 32 || tile_rows == 64 || tile_rows == 96 ||
                      tile_rows == 128,
                  "tile rows must be 0 (planned), 32, 64, 96 or 128");
+    ovg::Require(tile_cols == 0 || tile_cols == 128 || (tile_cols == 256 && tile_rows == 128),
+                 "tile columns must be 0 (planned), 128, or 256 with 128 rows");
+    ovg::Require((tile_rows == 0) == (tile_cols == 0), "force both tile sides or neither");
     auto s = static_cast<hipStream_t>(stream);
     const auto epi =
         accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;
@@ -180,8 +183,11 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
                                            static_cast<int>(in), epi);
     if (tile_rows != 0) {
       plan.xb = static_cast<int>(tile_rows / 32);
+      plan.wb = static_cast<int>(tile_cols / 128);
       plan.tiles = (static_cast<int>(rows) + static_cast<int>(tile_rows) - 1) /
-                   static_cast<int>(tile_rows) * ((static_cast<int>(out) + 127) / 128);
+                   static_cast<int>(tile_rows) *
+                   ((static_cast<int>(out) + static_cast<int>(tile_cols) - 1) /
+                    static_cast<int>(tile_cols));
     }
     ovg::GemmParams p{};
     p.x = static_cast<const ovg::half_t*>(x);

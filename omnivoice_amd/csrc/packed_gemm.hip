@@ -54,6 +54,8 @@
 // written out, so that the tile heights (template instantiations) round a
 // row's values identically.
 
+#include <algorithm>
+
 #include "kernels.hpp"
 
 #pragma clang fp contract(off)
@@ -86,6 +88,174 @@ __device__ __forceinline__ void Barrier() {
 
 // Keeps the compiler from moving memory operations across this point.
 __device__ __forceinline__ void AsmFence() { asm volatile("" : : : "memory"); }
+
+// Epilogue of one wave: its WB packed 32-column blocks block0 .. block0 +
+// WB - 1 (consecutive, inside one tile), accumulators acc[wb][b] for the
+// tile's 32-row blocks b. Every result is rounded the same way whatever XB
+// and WB are, so a row's outputs do not depend on the tile shape.
+template <int XB, int WB, Epilogue EPI>
+__device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc)[WB][XB],
+                                             int m0, int split, int block0, int wave,
+                                             int lane, unsigned char* lds) {
+  constexpr int kBM = 32 * XB;
+  const int h = lane >> 5;
+  const int col = lane & 31;
+  // Waves of a wide tile past the last column have nothing to store.
+  const bool live = block0 * 32 < p.n;
+  if constexpr (EPI == Epilogue::kStore || EPI == Epilogue::kAccumulate ||
+                EPI == Epilogue::kPartial) {
+    // Lane = column 32 block + lane % 32; element r of X block b is row
+    // 32 b + 8 (r / 4) + 4 (lane / 32) + r % 4.
+    float* y = p.y + (EPI == Epilogue::kPartial ? static_cast<size_t>(split) * p.split_stride : 0);
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb) {
+      const int n = (block0 + wb) * 32 + col;
+      if (n >= p.n)
+        continue;
+#pragma unroll
+      for (int b = 0; b < XB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m >= p.m)
+            continue;
+          float* dst = y + static_cast<size_t>(m) * p.ldc + n;
+          if constexpr (EPI == Epilogue::kAccumulate)
+            *dst = *dst + acc[wb][b][r];
+          else if constexpr (EPI == Epilogue::kPartial)
+            StoreThrough(dst, acc[wb][b][r]);
+          else
+            *dst = acc[wb][b][r];
+        }
+    }
+  } else if constexpr (EPI == Epilogue::kSwiGlu) {
+    // Block `block` holds gate and up of outputs 16 block .. 16 block + 15.
+    if (!live)
+      return;
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb) {
+      const int a_base = 16 * (block0 + wb) + 4 * h;
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int m = m0 + 32 * b + col;
+        if (m >= p.m)
+          continue;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          half4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float gate = acc[wb][b][4 * g + i];
+            const float up = acc[wb][b][4 * g + 8 + i];
+            v[i] = static_cast<half_t>(gate / (1.0F + __expf(-gate)) * up);
+          }
+          *reinterpret_cast<half4*>(p.act + static_cast<size_t>(m) * p.ldh + a_base + 8 * g) = v;
+        }
+      }
+    }
+  } else if constexpr (EPI == Epilogue::kQkvRope) {
+    // Block `block` is block % 4 of 128-column head block / 4; a head's four
+    // blocks belong to 4 / WB waves of the tile.
+    const int slot = block0 / 4;
+    const bool qk = live && slot < p.heads + p.kv_heads;
+    // Sum of squares of each block's 32 columns of a row, then over the
+    // head's four blocks in the fixed order (0 + 1) + (2 + 3): a wave adds
+    // its own pair when it holds two blocks, and the waves' sums meet in
+    // LDS (the K loop's last barrier separates the LDS reads of X from
+    // these writes).
+    float* sums = reinterpret_cast<float*>(lds);  // [4][kBM]
+    if (qk) {
+      float part[WB][XB];
+#pragma unroll
+      for (int wb = 0; wb < WB; ++wb)
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          float s = acc[wb][b][0] * acc[wb][b][0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r)
+            s = __builtin_fmaf(acc[wb][b][r], acc[wb][b][r], s);
+          part[wb][b] = s + __shfl_xor(s, 32);
+        }
+      if (h == 0) {
+#pragma unroll
+        for (int b = 0; b < XB; ++b)
+          sums[wave * kBM + 32 * b + col] = WB == 2 ? part[0][b] + part[WB - 1][b] : part[0][b];
+      }
+    }
+    __syncthreads();
+    if (qk) {
+      const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
+      // The first of the waves that hold this head.
+      const int first = WB == 2 ? (wave & ~1) : 0;
+      float scale[XB];
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int r_local = 32 * b + col;
+        const float total =
+            WB == 2 ? sums[first * kBM + r_local] + sums[(first + 1) * kBM + r_local]
+                    : (sums[r_local] + sums[kBM + r_local]) +
+                          (sums[2 * kBM + r_local] + sums[3 * kBM + r_local]);
+        scale[b] = rsqrtf(__builtin_fmaf(total, 1.0F / 128.0F, p.eps));
+      }
+#pragma unroll
+      for (int wb = 0; wb < WB; ++wb) {
+        // This lane's rotary indices: c = 16 (block % 4) + 8 g + 4 h + i, g < 2.
+        const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
+        float w_lo[2][4], w_hi[2][4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            w_lo[g][i] = weight[c_base + 8 * g + i];
+            w_hi[g][i] = weight[64 + c_base + 8 * g + i];
+          }
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          const int m = m0 + 32 * b + col;
+          if (m >= p.m)
+            continue;
+          const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
+          half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + c_base;
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            half4 lo, hi;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float2 rot = cs[8 * g + i];
+              const float a = w_lo[g][i] * (acc[wb][b][4 * g + i] * scale[b]);
+              const float bb = w_hi[g][i] * (acc[wb][b][4 * g + 8 + i] * scale[b]);
+              lo[i] = static_cast<half_t>(__builtin_fmaf(a, rot.x, -(bb * rot.y)));
+              hi[i] = static_cast<half_t>(__builtin_fmaf(bb, rot.x, a * rot.y));
+            }
+            *reinterpret_cast<half4*>(out + 8 * g) = lo;
+            *reinterpret_cast<half4*>(out + 64 + 8 * g) = hi;
+          }
+        }
+      }
+    } else if (live) {
+      // Value head gv: V^T[gv][d][VtColumn(row)], d the head column of the
+      // element (rope order inside the block).
+      const int gv = slot - p.heads - p.kv_heads;
+#pragma unroll
+      for (int wb = 0; wb < WB; ++wb) {
+        const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+          const int m = m0 + 32 * b + col;
+          if (m >= p.m)
+            continue;
+          const int column = VtColumn(m);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
+            p.vt[static_cast<size_t>(gv * 128 + d) * p.ldvt + column] =
+                static_cast<half_t>(acc[wb][b][r]);
+          }
+        }
+      }
+    }
+  }
+}
 
 template <int XB, Epilogue EPI>
 __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_m,
@@ -145,10 +315,10 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
       x_read[b][j] = row * 128 + Swizzle(row, 4 * (lane >> 5) + j) * 16;
     }
 
-  floatx16 acc[XB];
+  floatx16 acc[1][XB];
 #pragma unroll
   for (int b = 0; b < XB; ++b)
-    acc[b] = floatx16{};
+    acc[0][b] = floatx16{};
 
   half8 wf[4][4];       // W of steps t .. t + 3, slot t % 4
   half8 xs[2][XB];      // X of steps t + 2 and t + 3, slot t % 2
@@ -219,8 +389,8 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int b = 0; b < XB; ++b)
-        acc[b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[b])
-                           : Mfma32(fr[xo][j][b], wf[ws][j], acc[b]);
+        acc[0][b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[0][b])
+                              : Mfma32(fr[xo][j][b], wf[ws][j], acc[0][b]);
       __builtin_amdgcn_sched_barrier(0);
     }
     load_w(wf[ws], min(t + 4, last));
@@ -246,132 +416,166 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   if (whole + 2 < steps)
     step(whole + 2, I2{});
 
-  // ------------------------------------------------------------- epilogue
-  const int h = lane >> 5;
-  const int col = lane & 31;
-  if constexpr (EPI == Epilogue::kStore || EPI == Epilogue::kAccumulate ||
-                EPI == Epilogue::kPartial) {
-    // Lane = column 32 wave + lane % 32 of the tile; element r of X block b
-    // is row 32 b + 8 (r / 4) + 4 (lane / 32) + r % 4.
-    float* y = p.y + (EPI == Epilogue::kPartial ? static_cast<size_t>(split) * p.split_stride : 0);
-    const int n = tile_n * 128 + 32 * wave + col;
-    if (n < p.n) {
+  WaveEpilogue<XB, 1, EPI>(p, acc, m0, split, block, wave, lane, lds);
+}
+
+// The wide tile for large M: 128 x 256, each wave owning two packed blocks
+// (64 columns), so every X fragment read from LDS feeds two MFMAs (half the
+// LDS reads per MFMA of the 128 x 128 tile, which at large M is bound by
+// them). Registers: W two K steps ahead (a ring of two) and X fragments one
+// 16-wide substep ahead, with the eight MFMAs of a substep covering the
+// fragment reads' latency.
+template <Epilogue EPI>
+__global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_m, int k_steps) {
+  constexpr int XB = 4;
+  constexpr int WB = 2;
+  using S = Packed<XB>;
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr bool kRowLanes = EPI == Epilogue::kQkvRope || EPI == Epilogue::kSwiGlu;
+
+  const int groups = gridDim.x;
+  const int pid = blockIdx.x;
+  const int xcd = pid % kXcds;
+  const int per = groups / kXcds;
+  const int extra = groups % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + pid / kXcds;
+  const int tile_m = logical % tiles_m;
+  const int rest = logical / tiles_m;
+  const int split = rest % p.splits;
+  const int tile_n = rest / p.splits;
+  if (tile_n * 256 >= p.n)
+    return;
+  const int m0 = tile_m * S::kBM;
+  const int steps = k_steps / p.splits;
+  const int t0 = split * steps;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int block0 = tile_n * 8 + 2 * wave;  // this wave's two packed blocks
+
+  const half8* x_src[XB];
+  int x_dst[XB];
 #pragma unroll
-      for (int b = 0; b < XB; ++b)
+  for (int i = 0; i < XB; ++i) {
+    const int row = 8 * (XB * wave + i) + (lane >> 3);
+    x_src[i] = reinterpret_cast<const half8*>(
+        p.x + static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda + t0 * 64) + (lane & 7);
+    x_dst[i] = row * 128 + Swizzle(row, lane & 7) * 16;
+  }
+  // Block block0 + 1 follows block0 at k_steps * 256 half8.
+  const half8* w_src =
+      reinterpret_cast<const half8*>(p.w) + (static_cast<size_t>(block0) * k_steps + t0) * 256 + lane;
+  const size_t w_next = static_cast<size_t>(k_steps) * 256;
+  int x_read[XB][4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + 32 * b + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (m >= p.m)
-            continue;
-          float* dst = y + static_cast<size_t>(m) * p.ldc + n;
-          if constexpr (EPI == Epilogue::kAccumulate)
-            *dst = *dst + acc[b][r];
-          else if constexpr (EPI == Epilogue::kPartial)
-            StoreThrough(dst, acc[b][r]);
-          else
-            *dst = acc[b][r];
-        }
+  for (int b = 0; b < XB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 32 * b + (lane & 31);
+      x_read[b][j] = row * 128 + Swizzle(row, 4 * (lane >> 5) + j) * 16;
     }
-  } else if constexpr (EPI == Epilogue::kSwiGlu) {
-    // Block `block` holds gate and up of outputs 16 block .. 16 block + 15.
-    const int a_base = 16 * block + 4 * h;
+
+  floatx16 acc[WB][XB];
 #pragma unroll
-    for (int b = 0; b < XB; ++b) {
-      const int m = m0 + 32 * b + col;
-      if (m >= p.m)
-        continue;
+  for (int wb = 0; wb < WB; ++wb)
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        half4 v;
+    for (int b = 0; b < XB; ++b)
+      acc[wb][b] = floatx16{};
+
+  half8 wf[2][WB][4];  // W of steps t, t + 1, slot t % 2
+  half8 xs[2][XB];     // X of steps t + 2 and t + 3, slot t % 2
+  half8 fr[2][XB];     // X fragments of the current and the next substep
+  auto load_w = [&](half8 (&dst)[WB][4], int t) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gate = acc[b][4 * g + i];
-          const float up = acc[b][4 * g + 8 + i];
-          v[i] = static_cast<half_t>(gate / (1.0F + __expf(-gate)) * up);
-        }
-        *reinterpret_cast<half4*>(p.act + static_cast<size_t>(m) * p.ldh + a_base + 8 * g) = v;
-      }
-    }
-  } else if constexpr (EPI == Epilogue::kQkvRope) {
-    const int slot = tile_n;  // one 128-column head per tile
-    if (slot < p.heads + p.kv_heads) {
-      // Sum of squares of the wave's 32 columns of each row, then of the
-      // four waves in a fixed order.
-      float* sums = reinterpret_cast<float*>(lds);  // [4][kBM]
-      float part[XB];
+    for (int wb = 0; wb < WB; ++wb)
 #pragma unroll
-      for (int b = 0; b < XB; ++b) {
-        float s = acc[b][0] * acc[b][0];
+      for (int j = 0; j < 4; ++j)
+        dst[wb][j] = w_src[wb * w_next + (t * 4 + j) * 64];
+  };
+  auto load_x = [&](half8 (&dst)[XB], int t) {
 #pragma unroll
-        for (int r = 1; r < 16; ++r)
-          s = __builtin_fmaf(acc[b][r], acc[b][r], s);
-        part[b] = s + __shfl_xor(s, 32);
-      }
-      // The K loop's last barrier separates the LDS reads of X from these
-      // writes.
-      if (h == 0) {
+    for (int i = 0; i < XB; ++i)
+      dst[i] = x_src[i][t * 8];
+  };
+  auto store_x = [&](const half8 (&src)[XB], int buf) {
+#pragma unroll
+    for (int i = 0; i < XB; ++i)
+      *reinterpret_cast<half8*>(lds + buf * S::kStageBytes + x_dst[i]) = src[i];
+  };
+  auto read_frag = [&](half8 (&dst)[XB], int buf, int j) {
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+      dst[b] = *reinterpret_cast<const half8*>(lds + buf * S::kStageBytes + x_read[b][j]);
+  };
+
+  // Prologue: W of steps 0 and 1, X of steps 0 .. 3 (X(0), X(1) to LDS
+  // buffers 0 and 1), then the fragments of step 0's first substep. Step
+  // indices past the last are clamped (in-bounds reloads never used).
+  const int last = steps - 1;
+  load_w(wf[0], 0);
+  load_w(wf[1], min(1, last));
+  {
+    half8 x0[XB], x1[XB];
+    load_x(x0, 0);
+    load_x(x1, min(1, last));
+    load_x(xs[0], min(2, last));
+    load_x(xs[1], min(3, last));
+    store_x(x0, 0);
+    store_x(x1, 1);
+  }
+  Barrier();
+  read_frag(fr[0], 0, 0);
+
+  // Step t: write X(t + 2) into LDS buffer (t + 2) % 4 and reload those
+  // registers with X(t + 4); for each substep j run its eight MFMAs from
+  // fragments in registers after issuing the reads of the next substep
+  // (substep j + 1 of buffer t % 4, or the first substep of step t + 1 from
+  // buffer (t + 1) % 4, written in step t - 1); reload W's slot with
+  // W(t + 2); end at a barrier that waits for all of the step's LDS
+  // operations. A buffer is rewritten two barriers after its last read.
+  auto step = [&](int t, auto slot) {
+    constexpr int ws = decltype(slot)::value;  // t % 4
+    constexpr int xo = ws & 1;                 // t % 2
+    store_x(xs[xo], (ws + 2) & 3);
+    AsmFence();
+    load_x(xs[xo], min(t + 4, last));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < 3)
+        read_frag(fr[(j + 1) & 1], ws, j + 1);
+      else
+        read_frag(fr[0], (ws + 1) & 3, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int wb = 0; wb < WB; ++wb)
 #pragma unroll
         for (int b = 0; b < XB; ++b)
-          sums[wave * S::kBM + 32 * b + col] = part[b];
-      }
-      __syncthreads();
-      const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
-      // This lane's rotary indices: c = 16 wave + 8 g + 4 h + i, g < 2.
-      const int c_base = 16 * wave + 4 * h;
-      float w_lo[2][4], w_hi[2][4];
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          w_lo[g][i] = weight[c_base + 8 * g + i];
-          w_hi[g][i] = weight[64 + c_base + 8 * g + i];
-        }
-#pragma unroll
-      for (int b = 0; b < XB; ++b) {
-        const int r_local = 32 * b + col;
-        const int m = m0 + r_local;
-        const float total = (sums[r_local] + sums[S::kBM + r_local]) +
-                            (sums[2 * S::kBM + r_local] + sums[3 * S::kBM + r_local]);
-        const float scale = rsqrtf(__builtin_fmaf(total, 1.0F / 128.0F, p.eps));
-        if (m >= p.m)
-          continue;
-        const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
-        half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + c_base;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          half4 lo, hi;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float2 rot = cs[8 * g + i];
-            const float a = w_lo[g][i] * (acc[b][4 * g + i] * scale);
-            const float bb = w_hi[g][i] * (acc[b][4 * g + 8 + i] * scale);
-            lo[i] = static_cast<half_t>(__builtin_fmaf(a, rot.x, -(bb * rot.y)));
-            hi[i] = static_cast<half_t>(__builtin_fmaf(bb, rot.x, a * rot.y));
-          }
-          *reinterpret_cast<half4*>(out + 8 * g) = lo;
-          *reinterpret_cast<half4*>(out + 64 + 8 * g) = hi;
-        }
-      }
-    } else {
-      // Value head gv: V^T[gv][d][VtColumn(row)], d the head column of the
-      // element (rope order inside the block).
-      const int gv = slot - p.heads - p.kv_heads;
-      const int c_base = 16 * wave + 4 * h;
-#pragma unroll
-      for (int b = 0; b < XB; ++b) {
-        const int m = m0 + 32 * b + col;
-        if (m >= p.m)
-          continue;
-        const int column = VtColumn(m);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
-          p.vt[static_cast<size_t>(gv * 128 + d) * p.ldvt + column] =
-              static_cast<half_t>(acc[b][r]);
-        }
-      }
+          acc[wb][b] = kRowLanes ? Mfma32(wf[xo][wb][j], fr[j & 1][b], acc[wb][b])
+                                 : Mfma32(fr[j & 1][b], wf[xo][wb][j], acc[wb][b]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    load_w(wf[xo], min(t + 2, last));
+    Barrier();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  const int whole = steps & ~3;
+  for (int t = 0; t < whole; t += 4) {
+    step(t, I0{});
+    step(t + 1, I1{});
+    step(t + 2, I2{});
+    step(t + 3, I3{});
   }
+  if (whole < steps)
+    step(whole, I0{});
+  if (whole + 1 < steps)
+    step(whole + 1, I1{});
+  if (whole + 2 < steps)
+    step(whole + 2, I2{});
+
+  WaveEpilogue<XB, WB, EPI>(p, acc, m0, split, block0, wave, lane, lds);
 }
 
 // Packs row-major fp16 W [rows][K] into the fragment order above: half8
@@ -416,7 +620,21 @@ void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t str
 }
 
 template <Epilogue EPI>
+void LaunchPackedWide(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  const int tiles_m = (p.m + 127) / 128;
+  const int tiles_n = (p.n + 255) / 256;
+  const int groups = tiles_m * tiles_n * p.splits;
+  Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
+  Dispatch(PackedWideKernel<EPI>, dim3(groups), dim3(256), Packed<4>::kLds, stream, true, true,
+           p, tiles_m, p.k / 64);
+}
+
+template <Epilogue EPI>
 void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  if (plan.wb == 2) {
+    LaunchPackedWide<EPI>(p, plan, stream);
+    return;
+  }
   switch (plan.xb) {
     case 1: LaunchPackedXB<1, EPI>(p, plan, stream); break;
     case 2: LaunchPackedXB<2, EPI>(p, plan, stream); break;
@@ -428,16 +646,16 @@ void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t st
 }  // namespace
 
 std::size_t PackedWeightHalves(int rows, int k) {
-  return static_cast<std::size_t>((rows + 127) / 128 * 128) * k;
+  return static_cast<std::size_t>((rows + 255) / 256 * 256) * k;
 }
 
 void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map,
                  half_t* out, hipStream_t stream) {
   Require(k % 64 == 0 && rows > 0, "pack: K must be a positive multiple of 64");
   Require(map != PackMap::kSwiGlu || w2 != nullptr, "pack: SwiGLU packing needs gate and up");
-  // Blocks of 32 columns, padded to whole 128-column tiles.
+  // Blocks of 32 columns, padded to whole 256-column tiles.
   const int out_rows = map == PackMap::kSwiGlu ? 2 * rows : rows;
-  const int blocks = (out_rows + 127) / 128 * 4;
+  const int blocks = (out_rows + 255) / 256 * 8;
   const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
   const int threads = 256;
   PackWeightsKernel<<<static_cast<unsigned>((total + threads - 1) / threads), threads, 0,
@@ -447,25 +665,35 @@ void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map
 
 PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   PackedPlan plan;
-  const int tiles_n = (n + 127) / 128;
   const int k_steps = k / 64;
   plan.splits = epilogue == Epilogue::kPartial ? PartialSplits(k_steps) : 1;
   const int steps = k_steps / plan.splits;
-  // The K loop is bound by the operands each CU pulls from L2 per K step
-  // (32 XB rows of X plus 128 columns of W: XB + 4 units of 4 KB); a tile
-  // also pays a fixed cost (first loads, epilogue) of about 50 units.
+  // Cycles per K step of one work-group, the largest of: the operands it
+  // pulls from L2 (32 XB rows of X and 128 WB columns of W, 128 bytes each,
+  // at 64 bytes per clock), its LDS traffic (X written once and read by
+  // four waves, at 128 bytes per clock) and its MFMAs (XB WB 4 per SIMD, 32
+  // clocks each); plus about 3200 clocks a tile (first loads, epilogue).
   // Estimated time: rounds of work-groups over the CUs times that.
+  struct Shape {
+    int xb, wb;
+  };
   double best = 0.0;
-  for (const int xb : {4, 3, 2, 1}) {
-    const int tiles = (m + 32 * xb - 1) / (32 * xb) * tiles_n * plan.splits;
+  for (const Shape sh : {Shape{4, 2}, Shape{4, 1}, Shape{3, 1}, Shape{2, 1}, Shape{1, 1}}) {
+    const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) *
+                      ((n + 128 * sh.wb - 1) / (128 * sh.wb)) * plan.splits;
     const int rounds = (tiles + kCus - 1) / kCus;
-    const double cost = rounds * (static_cast<double>(steps) * (xb + 4) + 50.0);
+    const double l2 = (32.0 * sh.xb + 128.0 * sh.wb) * 128.0 / 64.0;
+    const double lds = 5.0 * 32.0 * sh.xb * 128.0 / 128.0;
+    const double mfma = 4.0 * sh.xb * sh.wb * 32.0;
+    const double cost =
+        rounds * (static_cast<double>(steps) * std::max(l2, std::max(lds, mfma)) + 3200.0);
     if (best == 0.0 || cost < best) {
       best = cost;
-      plan.xb = xb;
+      plan.xb = sh.xb;
+      plan.wb = sh.wb;
+      plan.tiles = tiles / plan.splits;
     }
   }
-  plan.tiles = (m + 32 * plan.xb - 1) / (32 * plan.xb) * tiles_n;
   return plan;
 }
 
@@ -476,7 +704,8 @@ void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue
   Require(p.splits == plan.splits && (p.k / 64) % p.splits == 0,
           "gemm: K steps not divisible by the split count");
   Require(p.lda % 8 == 0, "gemm: the row stride of X must be a multiple of 8");
-  Require(plan.xb >= 1 && plan.xb <= 4, "gemm: tile height of 1 to 4 blocks of 32 rows");
+  Require(plan.xb >= 1 && plan.xb <= 4 && (plan.wb == 1 || (plan.wb == 2 && plan.xb == 4)),
+          "gemm: tile of 32 to 128 rows x 128 columns, or 128 x 256");
   switch (epilogue) {
     case Epilogue::kStore:
     case Epilogue::kAccumulate:

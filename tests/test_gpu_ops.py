@@ -129,9 +129,9 @@ def test_linear_matches_float64(rows, k, n, acc):
     (120, 1024, 4096, False), (580, 2048, 1024, True), (33, 512, 256, False),
     (500, 1024, 8200, False), (96, 384, 256, True), (1, 256, 128, False),
     (3440, 1024, 6144, False), (85, 256, 1024, False)])
-def test_packed_linear_matches_float64_at_every_tile_height(rows, k, n, acc):
+def test_packed_linear_matches_float64_at_every_tile(rows, k, n, acc):
     """The generator's packed-weight kernel against float64, at every tile
-    height, and bit-identical across heights (a row's result does not depend
+    shape, and bit-identical across shapes (a row's result does not depend
     on the tile the packed row count selects)."""
     rng = np.random.default_rng(rows + n + 7)
     x = rng.standard_normal((rows, k)).astype(np.float16)
@@ -142,12 +142,13 @@ def test_packed_linear_matches_float64_at_every_tile_height(rows, k, n, acc):
         want += y0
     scale = np.sqrt(k) * 0.02
     results = []
-    for tile_rows in (0, 32, 64, 96, 128):
+    for tile in ((0, 0), (32, 128), (64, 128), (96, 128), (128, 128), (128, 256)):
         y = dev(y0)
-        ov.op_linear_packed(dev(x), dev(w), y, accumulate=acc, tile_rows=tile_rows)
+        ov.op_linear_packed(dev(x), dev(w), y, accumulate=acc, tile_rows=tile[0],
+                            tile_cols=tile[1])
         got = host(y)
-        assert np.isfinite(got).all(), tile_rows
-        assert np.abs(got - want).max() < 1e-4 * scale * 10 + 1e-5, tile_rows
+        assert np.isfinite(got).all(), tile
+        assert np.abs(got - want).max() < 1e-4 * scale * 10 + 1e-5, tile
         results.append(got.tobytes())
     assert all(r == results[0] for r in results)
 

@@ -567,13 +567,16 @@ void Engine::Prepare(const Layout& L) {
   // packed rows, which no kernel writes: keep those K rows and V^T columns
   // zero, since a masked key's probability 0 times a non-finite stale value
   // would still be NaN. (Rows inside the packed range, alignment padding
-  // included, are written by the q/k/v GEMM every layer.)
+  // included, are written by the q/k/v GEMM every layer.) VtColumn permutes
+  // rows inside 16-row blocks, so the V^T clear starts at the block that
+  // holds the last packed row; the GEMM rewrites that block's own rows.
+  const int vt_clear = L.rows & ~15;
   Check(hipMemsetAsync(qk_.get() + static_cast<std::size_t>(L.rows) * qk_width, 0,
                        static_cast<std::size_t>(L.rows_alloc - L.rows) * qk_width * sizeof(half_t),
                        stream_),
         "clear key slack");
-  Check(hipMemset2DAsync(vt_.get() + L.rows, static_cast<std::size_t>(ldvt) * sizeof(half_t), 0,
-                         static_cast<std::size_t>(ldvt - L.rows) * sizeof(half_t),
+  Check(hipMemset2DAsync(vt_.get() + vt_clear, static_cast<std::size_t>(ldvt) * sizeof(half_t), 0,
+                         static_cast<std::size_t>(ldvt - vt_clear) * sizeof(half_t),
                          static_cast<std::size_t>(cfg_.kv_heads) * 128, stream_),
         "clear value slack");
   auto up = [&](void* dst, const void* src, std::size_t bytes) {

@@ -130,15 +130,18 @@ int PartialSplits(int k_steps);
 // and ldb is unused.
 enum class PackMap : int {
   kIdentity = 0,  // block column i = output column i
-  kRope = 1,      // 128-column heads: block w holds head columns 16 w .. +15
-                  // and 64 + 16 w .. +15 (rotate-half pairs in one lane)
+  kRope = 1,      // q/k/v: 128-column heads in kv-group order (each kv
+                  // head's `group` query heads, then its k and v heads);
+                  // block w of a head holds head columns 16 w .. +15 and
+                  // 64 + 16 w .. +15 (rotate-half pairs in one lane)
   kSwiGlu = 2,    // block b holds gate rows 16 b .. +15 then up rows 16 b .. +15
 };
 // Halves a packed copy of a [rows][k] matrix takes (rows padded to 256).
 std::size_t PackedWeightHalves(int rows, int k);
 // Packs row-major fp16 w [rows][k] (for kSwiGlu: gate w and up w2, [rows][k]
-// each, packed as 2 rows outputs) on the device.
-void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map,
+// each, packed as 2 rows outputs; for kRope: [q; k; v] heads, `group` query
+// heads per kv head) on the device.
+void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
                  half_t* out, hipStream_t stream);
 struct PackedPlan {
   int xb = 4;      // tile height in 32-row blocks

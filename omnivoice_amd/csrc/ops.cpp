@@ -178,7 +178,7 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
     Scratch<ovg::half_t> packed(ovg::PackedWeightHalves(static_cast<int>(out),
                                                         static_cast<int>(in)));
     ovg::PackWeights(static_cast<const ovg::half_t*>(w), nullptr, static_cast<int>(out),
-                     static_cast<int>(in), ovg::PackMap::kIdentity, packed.data, s);
+                     static_cast<int>(in), ovg::PackMap::kIdentity, 0, packed.data, s);
     ovg::PackedPlan plan = ovg::PlanPacked(static_cast<int>(rows), static_cast<int>(out),
                                            static_cast<int>(in), epi);
     if (tile_rows != 0) {

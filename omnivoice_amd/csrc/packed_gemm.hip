@@ -89,6 +89,21 @@ __device__ __forceinline__ void Barrier() {
 // Keeps the compiler from moving memory operations across this point.
 __device__ __forceinline__ void AsmFence() { asm volatile("" : : : "memory"); }
 
+// Packed q/k/v column tile (128-column head) `slot` in kv-group order: the
+// `group` query heads of kv head g, then its key head, then its value head,
+// for g = 0, 1, ... Returns the head's index in the reference's row order
+// [q heads; k heads; v heads] (-1 past the last of `total` heads). With the
+// tiles in this order the GEMM's XCD-contiguous tile runs write one kv
+// group's q, k and v on one XCD, the XCD whose attention work-groups read
+// them.
+__host__ __device__ __forceinline__ int QkvHead(int slot, int total, int group) {
+  if (slot >= total)
+    return -1;
+  const int kv = total / (group + 2);
+  const int g = slot / (group + 2), j = slot % (group + 2);
+  return j < group ? g * group + j : j == group ? kv * group + g : kv * (group + 1) + g;
+}
+
 // Epilogue of one wave: its WB packed 32-column blocks block0 .. block0 +
 // WB - 1 (consecutive, inside one tile), accumulators acc[wb][b] for the
 // tile's 32-row blocks b. Every result is rounded the same way whatever XB
@@ -154,10 +169,11 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
       }
     }
   } else if constexpr (EPI == Epilogue::kQkvRope) {
-    // Block `block` is block % 4 of 128-column head block / 4; a head's four
-    // blocks belong to 4 / WB waves of the tile.
-    const int slot = block0 / 4;
-    const bool qk = live && slot < p.heads + p.kv_heads;
+    // Block `block` is block % 4 of packed head block / 4 (kv-group order,
+    // QkvHead); a head's four blocks belong to 4 / WB waves of the tile.
+    const int total = p.heads + 2 * p.kv_heads;
+    const int slot = QkvHead(block0 / 4, total, p.heads / p.kv_heads);
+    const bool qk = live && slot >= 0 && slot < p.heads + p.kv_heads;
     // Sum of squares of each block's 32 columns of a row, then over the
     // head's four blocks in the fixed order (0 + 1) + (2 + 3): a wave adds
     // its own pair when it holds two blocks, and the waves' sums meet in
@@ -232,7 +248,7 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           }
         }
       }
-    } else if (live) {
+    } else if (live && slot >= 0) {
       // Value head gv: V^T[gv][d][VtColumn(row)], d the head column of the
       // element (rope order inside the block).
       const int gv = slot - p.heads - p.kv_heads;
@@ -582,7 +598,7 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
 // number ((block K/64 + t) 4 + j) 64 + l holds W[row(block, l % 32)][64 t +
 // 32 (l / 32) + 8 j .. + 7]; rows past `rows` are zero. One thread per half8.
 __global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, int k,
-                                  int blocks, PackMap map, half8* out) {
+                                  int blocks, PackMap map, int group, half8* out) {
   const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
   const size_t o = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (o >= total)
@@ -596,8 +612,10 @@ __global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, i
   const half_t* src = w;
   int row = 32 * block + i;
   if (map == PackMap::kRope) {
-    const int head = block / 4, wv = block % 4;
-    row = 128 * head + (i < 16 ? 16 * wv + i : 64 + 16 * wv + (i - 16));
+    const int wv = block % 4;
+    const int head = QkvHead(block / 4, rows / 128, group);
+    row = head < 0 ? rows
+                   : 128 * head + (i < 16 ? 16 * wv + i : 64 + 16 * wv + (i - 16));
   } else if (map == PackMap::kSwiGlu) {
     row = 16 * block + (i & 15);
     src = i < 16 ? w : w2;
@@ -649,9 +667,11 @@ std::size_t PackedWeightHalves(int rows, int k) {
   return static_cast<std::size_t>((rows + 255) / 256 * 256) * k;
 }
 
-void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map,
+void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
                  half_t* out, hipStream_t stream) {
   Require(k % 64 == 0 && rows > 0, "pack: K must be a positive multiple of 64");
+  Require(map != PackMap::kRope || (group > 0 && rows % 128 == 0 && (rows / 128) % (group + 2) == 0),
+          "pack: q/k/v packing needs (group + 2) kv groups of 128-row heads");
   Require(map != PackMap::kSwiGlu || w2 != nullptr, "pack: SwiGLU packing needs gate and up");
   // Blocks of 32 columns, padded to whole 256-column tiles.
   const int out_rows = map == PackMap::kSwiGlu ? 2 * rows : rows;
@@ -659,7 +679,7 @@ void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map
   const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
   const int threads = 256;
   PackWeightsKernel<<<static_cast<unsigned>((total + threads - 1) / threads), threads, 0,
-                      stream>>>(w, w2, rows, k, blocks, map, reinterpret_cast<half8*>(out));
+                      stream>>>(w, w2, rows, k, blocks, map, group, reinterpret_cast<half8*>(out));
   Check(hipGetLastError(), "pack launch");
 }
 

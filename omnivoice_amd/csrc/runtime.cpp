@@ -240,7 +240,7 @@ void Engine::UploadPacked(DeviceBuffer<half_t>& dst, const std::vector<half_t>& 
   PackWeights(staging.get(),
               map == PackMap::kSwiGlu ? staging.get() + static_cast<std::size_t>(rows) * k
                                       : nullptr,
-              rows, k, map, dst.get(), stream_);
+              rows, k, map, static_cast<int>(cfg_.heads / cfg_.kv_heads), dst.get(), stream_);
   Check(hipStreamSynchronize(stream_), "pack weights");
 }
 

@@ -113,9 +113,42 @@ __device__ __forceinline__ Slice Merge(const Slice& a, const Slice& b) {
   return c;
 }
 
+// The prefetch work-groups: each thread keeps eight 16-byte loads in
+// flight (clamped in bounds, no load under a condition) and folds them into
+// a value that is never stored, so only the cache fill remains.
+__device__ __forceinline__ void PrefetchRanges(const AttentionParams& p, int group) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kInFlight = 8;
+  const unsigned long long stride = static_cast<unsigned long long>(p.prefetch_groups) * blockDim.x;
+  unsigned int fold = 0;
+  for (int r = 0; r < AttentionParams::kMaxPrefetch; ++r) {
+    const unsigned long long chunks = p.prefetch_bytes[r] / 16;
+    if (chunks == 0)
+      continue;
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.prefetch[r]);
+    for (unsigned long long c = static_cast<unsigned long long>(group) * blockDim.x + threadIdx.x;
+         c < chunks; c += kInFlight * stride) {
+      u32x4 v[kInFlight];
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        v[k] = src[min(c + k * stride, chunks - 1)];
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        fold ^= v[k].x;
+    }
+  }
+  // Never true (prefetch_groups > 0 here); keeps the loads alive.
+  if (fold == 0x9e3779b9u && p.prefetch_groups < 0)
+    p.out[0] = static_cast<half_t>(0.0F);
+}
+
 template <int GROUP>
 __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     AttentionParams p) {
+  if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
+    PrefetchRanges(p, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
+    return;
+  }
   constexpr int kWaves = 4 * GROUP;  // compute waves; wave kWaves: producer
   constexpr int kShare = 64 / kWaves;       // DMAs per wave and round
   constexpr int kQShare = 8 * GROUP / kWaves;  // query DMAs per wave
@@ -386,7 +419,8 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
               static_cast<uint64_t>(p.ldvt) * 2 * 64 < (uint64_t{1} << 31),
           "attention: rows too wide");
   const int group = p.heads / p.kv_heads;
-  const dim3 grid(p.work_count * p.kv_heads);
+  Require(p.prefetch_groups >= 0, "attention: negative prefetch group count");
+  const dim3 grid(p.work_count * p.kv_heads + p.prefetch_groups);
   switch (group) {
     case 1:
       Dispatch(AttentionKernel<1>, grid, dim3(5 * 64), AttentionLds<1>(), stream,

@@ -217,6 +217,13 @@ struct AttentionParams {
   int work_count;
   int ld_qk, ldvt, heads, kv_heads;
   float scale_log2;        // log2(e) / sqrt(128)
+  // Weight prefetch: `prefetch_groups` extra work-groups after the attention
+  // ones read these byte ranges (the weights of the GEMMs that follow), so
+  // that those GEMMs find them in the memory-side cache instead of HBM.
+  static constexpr int kMaxPrefetch = 5;
+  const unsigned char* prefetch[kMaxPrefetch];
+  unsigned long long prefetch_bytes[kMaxPrefetch];
+  int prefetch_groups;
 };
 void LaunchAttention(const AttentionParams& p, hipStream_t stream);
 

@@ -693,7 +693,11 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   // at 64 bytes per clock), its LDS traffic (X written once and read by
   // four waves, at 128 bytes per clock) and its MFMAs (XB WB 4 per SIMD, 32
   // clocks each); plus about 3200 clocks a tile (first loads, epilogue).
-  // Estimated time: rounds of work-groups over the CUs times that.
+  // Estimated time: rounds of work-groups over the CUs times that, where a
+  // last, partial round counts by its share of the CUs but at least half a
+  // round (fewer work-groups at once run faster each, but a few stragglers
+  // still cost most of a round: the 10 s audio heads run 20.4 us as 390
+  // 96-row tiles, 1.5 rounds, against 23.1 us as 132 wide tiles).
   struct Shape {
     int xb, wb;
   };
@@ -701,7 +705,10 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   for (const Shape sh : {Shape{4, 2}, Shape{4, 1}, Shape{3, 1}, Shape{2, 1}, Shape{1, 1}}) {
     const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) *
                       ((n + 128 * sh.wb - 1) / (128 * sh.wb)) * plan.splits;
-    const int rounds = (tiles + kCus - 1) / kCus;
+    const int full = tiles / kCus, rest = tiles % kCus;
+    const double rounds =
+        full == 0 ? 1.0
+                  : full + (rest == 0 ? 0.0 : std::max(0.5, static_cast<double>(rest) / kCus));
     const double l2 = (32.0 * sh.xb + 128.0 * sh.wb) * 128.0 / 64.0;
     const double lds = 5.0 * 32.0 * sh.xb * 128.0 / 128.0;
     const double mfma = 4.0 * sh.xb * sh.wb * 32.0;

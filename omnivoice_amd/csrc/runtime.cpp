@@ -706,6 +706,27 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
            p.kv_heads = static_cast<int>(cfg_.kv_heads);
            p.eps = cfg_.rms_norm_eps;
          });
+    // The attention leaves CUs idle (one work-group per query tile and kv
+    // head): extra work-groups pull this layer's o, gate/up and down weights
+    // and the next layer's q/k/v (after the last layer: the audio heads and
+    // layer 0's q/k/v) into the memory-side cache, from which the GEMMs then
+    // stream them.
+    {
+      const Layer& next = layers_[(l + 1) % layers_.size()];
+      const DeviceBuffer<half_t>* ranges[AttentionParams::kMaxPrefetch] = {
+          &W.output, &W.gate_up, &W.down, l + 1 < layers_.size() ? &next.qkv : &heads_,
+          l + 1 < layers_.size() ? nullptr : &next.qkv};
+      for (int r = 0; r < AttentionParams::kMaxPrefetch; ++r) {
+        ap.prefetch[r] = ranges[r] ? reinterpret_cast<const unsigned char*>(ranges[r]->get())
+                                   : nullptr;
+        ap.prefetch_bytes[r] = ranges[r] ? ranges[r]->bytes() : 0;
+      }
+      // Only where at least a quarter of the CUs would idle: with fewer
+      // prefetch work-groups the reads outlast the attention and delay
+      // everything after it (clone and chunk shapes, measured).
+      const int busy = ap.work_count * ap.kv_heads;
+      ap.prefetch_groups = busy <= 192 ? 256 - busy : 0;
+    }
     Run(prof, "attention", attention_flops, R * (qkv_n + heads_width) * 2.0,
         [&] { LaunchAttention(ap, stream_); });
     gemm("gemm_o_partial", Epilogue::kPartial, attn_.get(), heads_width,

@@ -366,16 +366,24 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   // are never used), so that no load sits under a condition: a conditional
   // load makes the compiler's wait counts assume it was skipped and wait for
   // the loads before it.
+  //
+  // The loads are issued in the loop's own order (X of a step, then W of
+  // that step), so that at the loop's first step the loads in flight are
+  // those of its steady state: the compiler's wait counts at the loop head
+  // are the smaller of what the first iteration and the later ones need, and
+  // a prologue in another order made two steps in four wait for loads issued
+  // one step earlier instead of two.
   const int last = steps - 1;
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    load_w(wf[s], min(s, last));
   {
     half8 x0[XB], x1[XB];
+    load_w(wf[0], 0);
+    load_w(wf[1], min(1, last));
     load_x(x0, 0);
     load_x(x1, min(1, last));
     load_x(xs[0], min(2, last));
+    load_w(wf[2], min(2, last));
     load_x(xs[1], min(3, last));
+    load_w(wf[3], min(3, last));
     store_x(x0, 0);
     store_x(x1, 1);
   }
@@ -527,15 +535,18 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   // Prologue: W of steps 0 and 1, X of steps 0 .. 3 (X(0), X(1) to LDS
   // buffers 0 and 1), then the fragments of step 0's first substep. Step
   // indices past the last are clamped (in-bounds reloads never used).
+  // Loads in the loop's own order (X of step t + 4, then W of step t + 2),
+  // so that the compiler's wait counts at the loop head are those of the
+  // steady state.
   const int last = steps - 1;
-  load_w(wf[0], 0);
-  load_w(wf[1], min(1, last));
   {
     half8 x0[XB], x1[XB];
     load_x(x0, 0);
     load_x(x1, min(1, last));
     load_x(xs[0], min(2, last));
+    load_w(wf[0], 0);
     load_x(xs[1], min(3, last));
+    load_w(wf[1], min(1, last));
     store_x(x0, 0);
     store_x(x1, 1);
   }

@@ -300,8 +300,9 @@ def gemm_compare(args, torch):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=60,
-                    help="utterances timed (each one Generate call of 32 unmasking steps)")
+    ap.add_argument("--steps", type=int, default=200,
+                    help="utterances timed (each one Generate call of 32 unmasking steps; "
+                         "200 at 10 s keep the GPU busy for ~12 s)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="10s", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0,

@@ -65,9 +65,10 @@ enum class Epilogue : int {
   kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
                     // qk [M][ldq]; v heads -> fp16 V^T
                     // vt[g][d][VtColumn(row)] (ldvt % 16 == 0)
-  kSwiGlu = 3,      // W rows interleaved per 128-row tile as 64 gate rows
-                    // then the matching 64 up rows; act fp16 [M][ldh] =
-                    // silu(gate) * up
+  kSwiGlu = 3,      // act fp16 [M][ldh] = silu(gate) * up; the W rows pair
+                    // gate and up rows: per 128-row tile 64 gate rows then
+                    // the matching 64 up rows (GemmKernel), or per packed
+                    // 32-row block 16 and 16 (PackMap::kSwiGlu)
   kPartial = 4,     // split s stores its fp32 tile to y + s * split_stride
                     // ([M][ldc] per split); a row kernel sums the splits
 };

@@ -57,29 +57,6 @@ constexpr int AttentionLds() {
   return ring > merge ? ring : merge;
 }
 
-__device__ __forceinline__ uint32_t LdsAddress(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (const __attribute__((address_space(3))) unsigned char*)(p)));
-}
-
-// Wave-wide DMA of 64 x 16 bytes into LDS (lane l's bytes land at
-// lds_addr + 16 l) from a wave-uniform base plus a per-lane byte offset.
-__device__ __forceinline__ void DmaToLds(const unsigned char* base,
-                                         uint32_t offset, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2"
-      :
-      : "s"(lds_addr), "v"(offset), "s"(base)
-      : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void WaitLoads() {
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
 // Barrier without the fence of __syncthreads(), which would wait for every
 // DMA in flight.
 __device__ __forceinline__ void RingBarrier() {

@@ -96,6 +96,37 @@ __device__ __forceinline__ float WaveMax(float v) {
   return v;
 }
 
+// LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
+__device__ __forceinline__ uint32_t LdsAddress(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) unsigned char*)(p)));
+}
+
+// One wave-wide DMA of 64 x 16 bytes from global memory straight into LDS:
+// lane l's 16 bytes land at lds_addr + 16 l. Inline assembly because the
+// compiler's wait-count pass cannot tell which stage buffer such a load
+// writes and would wait for every load in flight before any LDS read, which
+// serialises a ring; the kernels wait explicitly instead (WaitLoads).
+// The source is a wave-uniform base (scalar registers) plus a per-lane
+// 32-bit byte offset, so that advancing a K step is one scalar add and the
+// LDS address is scalar too: no vector work per DMA.
+__device__ __forceinline__ void DmaToLds(const unsigned char* base, uint32_t offset,
+                                         uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(lds_addr), "v"(offset), "s"(base)
+      : "memory", "m0");
+}
+
+// Waits until at most N of this wave's vector memory loads are in flight.
+template <int N>
+__device__ __forceinline__ void WaitLoads() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 // 32x32x16 fp16 MFMA (gfx950): D = A B + C. Lane l supplies
 // A[l % 32][8 (l / 32) .. +7] and B[8 (l / 32) .. +7][l % 32]; it receives
 // D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] in element r.

@@ -91,43 +91,12 @@ constexpr int LdsBytes() {
 }
 static_assert(LdsBytes<3, 2>() <= 160 * 1024, "LDS budget");
 
-// LDS address (byte offset in the work-group's LDS) of a __shared__ pointer.
-__device__ __forceinline__ uint32_t LdsAddress(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (const __attribute__((address_space(3))) unsigned char*)(p)));
-}
-
 // Operand stages are [rows][64 halves]: 128-byte rows, no padding. The
 // 16-byte chunk c of row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1):
 // the 32 rows a fragment read touches then fall on distinct banks in both
 // 8-lane (128-byte) and 16-lane (256-byte) LDS phases. Its own inverse.
 __device__ __forceinline__ int Swizzle(int row, int chunk) {
   return chunk ^ (row & 7) ^ ((row >> 3) & 1);
-}
-
-// One wave-wide DMA of 64 x 16 bytes from global memory straight into LDS:
-// lane l's 16 bytes land at lds_addr + 16 l. Inline assembly because the
-// compiler's wait-count pass cannot tell which stage buffer such a load
-// writes and would wait for every load in flight before any LDS read, which
-// serialises the ring; the kernel waits explicitly instead.
-// The source is a wave-uniform base (scalar registers) plus a per-lane
-// 32-bit byte offset, so that advancing a K step is one scalar add and the
-// LDS address is scalar too: no vector work per DMA.
-__device__ __forceinline__ void DmaToLds(const unsigned char* base,
-                                         uint32_t offset, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2"
-      :
-      : "s"(lds_addr), "v"(offset), "s"(base)
-      : "memory", "m0");
-}
-
-// Waits until at most N of this wave's vector memory loads are in flight.
-template <int N>
-__device__ __forceinline__ void WaitLoads() {
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
 // Barrier without the memory fence __syncthreads() carries (that fence

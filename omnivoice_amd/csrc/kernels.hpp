@@ -145,8 +145,8 @@ std::size_t PackedWeightHalves(int rows, int k);
 void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
                  half_t* out, hipStream_t stream);
 struct PackedPlan {
-  int xb = 4;      // tile height in 32-row blocks
-  int wb = 1;      // tile width in 128-column units (2: the 128 x 256 tile)
+  int xb = 4;      // tile height in 32-row blocks (1-4, or 8 with wb 2)
+  int wb = 1;      // tile width in 128-column units (2: 128 x 256 or 256 x 256)
   int splits = 1;  // K split (partial-slice epilogue only)
   int tiles = 0;   // row tiles x column tiles
 };

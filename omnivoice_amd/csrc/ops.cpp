@@ -166,12 +166,11 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
     ovg::Require(rows >= 1 && in >= 64 && out >= 1 && FitsInt(rows) &&
                      FitsInt(in) && FitsInt(out),
                  "empty or oversized shape");
-    ovg::Require(tile_rows == 0 || tile_rows == 32 || tile_rows == 64 || tile_rows == 96 ||
-                     tile_rows == 128,
-                 "tile rows must be 0 (planned), 32, 64, 96 or 128");
-    ovg::Require(tile_cols == 0 || tile_cols == 128 || (tile_cols == 256 && tile_rows == 128),
-                 "tile columns must be 0 (planned), 128, or 256 with 128 rows");
-    ovg::Require((tile_rows == 0) == (tile_cols == 0), "force both tile sides or neither");
+    const bool narrow = tile_cols == 128 && (tile_rows == 32 || tile_rows == 64 ||
+                                             tile_rows == 96 || tile_rows == 128);
+    const bool wide = tile_cols == 256 && (tile_rows == 128 || tile_rows == 256);
+    ovg::Require((tile_rows == 0 && tile_cols == 0) || narrow || wide,
+                 "tile must be 0 x 0 (planned), 32/64/96/128 x 128, 128 x 256 or 256 x 256");
     auto s = static_cast<hipStream_t>(stream);
     const auto epi =
         accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;

@@ -176,12 +176,12 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
     const bool qk = live && slot >= 0 && slot < p.heads + p.kv_heads;
     // Sum of squares of each block's 32 columns of a row, then over the
     // head's four blocks in the fixed order (0 + 1) + (2 + 3): a wave adds
-    // its own pair when it holds two blocks, and the waves' sums meet in
-    // LDS (the K loop's last barrier separates the LDS reads of X from
-    // these writes).
+    // its own pair when it holds two blocks, or all four when it holds the
+    // head, and otherwise the waves' sums meet in LDS (the K loop's last
+    // barrier separates the LDS reads of X from these writes).
     float* sums = reinterpret_cast<float*>(lds);  // [4][kBM]
+    float part[WB][XB];
     if (qk) {
-      float part[WB][XB];
 #pragma unroll
       for (int wb = 0; wb < WB; ++wb)
 #pragma unroll
@@ -192,7 +192,7 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
             s = __builtin_fmaf(acc[wb][b][r], acc[wb][b][r], s);
           part[wb][b] = s + __shfl_xor(s, 32);
         }
-      if (h == 0) {
+      if (WB < 4 && h == 0) {
 #pragma unroll
         for (int b = 0; b < XB; ++b)
           sums[wave * kBM + 32 * b + col] = WB == 2 ? part[0][b] + part[WB - 1][b] : part[0][b];
@@ -207,10 +207,14 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
 #pragma unroll
       for (int b = 0; b < XB; ++b) {
         const int r_local = 32 * b + col;
-        const float total =
-            WB == 2 ? sums[first * kBM + r_local] + sums[(first + 1) * kBM + r_local]
-                    : (sums[r_local] + sums[kBM + r_local]) +
-                          (sums[2 * kBM + r_local] + sums[3 * kBM + r_local]);
+        float total;
+        if constexpr (WB == 4)
+          total = (part[0][b] + part[1][b]) + (part[2][b] + part[3][b]);
+        else if constexpr (WB == 2)
+          total = sums[first * kBM + r_local] + sums[(first + 1) * kBM + r_local];
+        else
+          total = (sums[r_local] + sums[kBM + r_local]) +
+                  (sums[2 * kBM + r_local] + sums[3 * kBM + r_local]);
         scale[b] = rsqrtf(__builtin_fmaf(total, 1.0F / 128.0F, p.eps));
       }
 #pragma unroll
@@ -605,6 +609,212 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   WaveEpilogue<XB, WB, EPI>(p, acc, m0, split, block0, wave, lane, lds);
 }
 
+// The large tile for large M: 256 x 256, four waves in a 2 x 2 arrangement,
+// wave w owning rows 128 (w / 2) .. + 127 and the four packed blocks
+// 4 (w % 2) .. + 3, 16 accumulators. Every fragment read from LDS feeds four
+// MFMAs, and the operands a work-group pulls from L2 per K step serve twice
+// the MFMAs of the 128 x 256 tile. X and W both go global -> LDS by DMA
+// (no registers, so a deep prefetch costs nothing but LDS) through a ring of
+// four half-steps (32 K values, 32 KB: X then W); a half-step's DMAs are
+// issued four half-steps before its MFMAs.
+//
+// Half-step s holds K substeps 2 (s % 2) and 2 (s % 2) + 1 of K step s / 2,
+// i.e. the 16-byte chunks {0, 1, 4, 5} or {2, 3, 6, 7} of every 128-byte
+// X row segment (lane half h supplies chunk 4 h + j in substep j, as in the
+// packed W): LDS X row r (64 bytes) holds those four chunks as positions
+// q = 2 h + (j % 2), at Swizzle32(r, q). The packed W of half-step s is 2 KB
+// of each block's 4 KB K step, copied verbatim.
+constexpr int kBigHalf = 32768;         // one half-step: X 16 KB, then W 16 KB
+constexpr int kBigLds = 4 * kBigHalf;   // ring of four half-steps
+constexpr int kBigDmas = 8;             // DMAs per wave per half-step
+
+// Position of chunk q of 64-byte LDS row r: distinct banks for the rows of
+// a fragment read in both 8-lane (128-byte) and 16-lane (256-byte) phases.
+// Its own inverse.
+__device__ __forceinline__ int Swizzle32(int row, int q) {
+  return q ^ ((row >> 1) & 3) ^ ((row >> 3) & 1);
+}
+
+template <Epilogue EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void PackedBigKernel(GemmParams p, int tiles_m, int k_steps) {
+  constexpr int XB = 4;
+  constexpr int WB = 4;
+  extern __shared__ __align__(16) unsigned char lds[];
+  constexpr bool kRowLanes = EPI == Epilogue::kQkvRope || EPI == Epilogue::kSwiGlu;
+
+  const int groups = gridDim.x;
+  const int pid = blockIdx.x;
+  const int xcd = pid % kXcds;
+  const int per = groups / kXcds;
+  const int extra = groups % kXcds;
+  const int logical = xcd * per + min(xcd, extra) + pid / kXcds;
+  const int tile_m = logical % tiles_m;
+  const int rest = logical / tiles_m;
+  const int split = rest % p.splits;
+  const int tile_n = rest / p.splits;
+  if (tile_n * 256 >= p.n)
+    return;
+  const int m0 = tile_m * 256;
+  const int steps = k_steps / p.splits;  // K steps of this split
+  const int t0 = split * steps;
+  const int halves = 2 * steps;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = wave >> 1;
+  const int wc = wave & 1;
+  const uint32_t lds0 = LdsAddress(lds);
+
+  // DMA sources. X: this wave brings LDS rows 64 w + 16 d + l / 4 (d < 4),
+  // lane l filling position l % 4 with the chunk that belongs there; rows
+  // past M read row M - 1 (never stored). W: blocks 2 w and 2 w + 1 of the
+  // tile, 2 KB each (two DMAs). Half-step s adds (s / 2) 128 + (s % 2) 32
+  // bytes to the X base and (s / 2) 4096 + (s % 2) 2048 to the W base.
+  const unsigned char* x_base =
+      reinterpret_cast<const unsigned char*>(p.x) + static_cast<size_t>(t0) * 128;
+  uint32_t x_off[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int row = 64 * wave + 16 * d + (lane >> 2);
+    const int q = Swizzle32(row, lane & 3);
+    const int chunk = (q & 1) + 4 * (q >> 1);
+    x_off[d] = static_cast<uint32_t>(
+        (static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda + 8 * chunk) * 2);
+  }
+  const unsigned char* w_base =
+      reinterpret_cast<const unsigned char*>(p.w) +
+      (static_cast<size_t>(tile_n * 8 + 2 * wave) * k_steps + t0) * 4096;
+  const uint32_t w_off0 = static_cast<uint32_t>(lane * 16);
+  const uint32_t w_off1 = w_off0 + static_cast<uint32_t>(k_steps) * 4096;
+
+  // DMA i (< 8) of half-step s into ring slot `slot`: X rows 16 i .. of this
+  // wave's 64 (i < 4), or 1 KB of W blocks 2 w + (i - 4) / 2.
+  auto dma_one = [&](int slot, int s, int i) {
+    const uint32_t stage = lds0 + slot * kBigHalf;
+    if (i < 4) {
+      DmaToLds(x_base + (s >> 1) * 128 + (s & 1) * 32, x_off[i], stage + wave * 4096 + i * 1024);
+    } else {
+      const unsigned char* ws = w_base + (s >> 1) * 4096 + (s & 1) * 2048 + (i & 1) * 1024;
+      DmaToLds(ws, i < 6 ? w_off0 : w_off1, stage + 16384 + wave * 4096 + (i - 4) * 1024);
+    }
+  };
+  auto dma = [&](int slot, int s) {
+#pragma unroll
+    for (int i = 0; i < kBigDmas; ++i)
+      dma_one(slot, s, i);
+  };
+
+  // Fragment reads: X row 128 wr + 32 b + lane % 32, position 2 h + jj;
+  // W block 4 wc + wb, substep jj, lane's 16 bytes.
+  int x_read[XB][2];
+#pragma unroll
+  for (int b = 0; b < XB; ++b)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int row = 128 * wr + 32 * b + (lane & 31);
+      x_read[b][jj] = row * 64 + Swizzle32(row, 2 * (lane >> 5) + jj) * 16;
+    }
+  const int w_read = 16384 + wc * 8192 + lane * 16;
+
+  floatx16 acc[WB][XB];
+#pragma unroll
+  for (int wb = 0; wb < WB; ++wb)
+#pragma unroll
+    for (int b = 0; b < XB; ++b)
+      acc[wb][b] = floatx16{};
+
+  half8 fx[2][XB];  // X fragments of the current and the next substep
+  half8 fw[2][WB];  // W fragments likewise
+  // Fragment read r (< 8) into set f: X fragment r (r < 4) or W fragment
+  // r - 4, of substep jj of ring slot `slot`.
+  auto read_one = [&](int f, int slot, int jj, int r) {
+    const unsigned char* stage = lds + slot * kBigHalf;
+    if (r < 4)
+      fx[f][r] = *reinterpret_cast<const half8*>(stage + x_read[r][jj]);
+    else
+      fw[f][r - 4] = *reinterpret_cast<const half8*>(stage + w_read + (r - 4) * 2048 + jj * 1024);
+  };
+  auto read_frag = [&](int f, int slot, int jj) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      read_one(f, slot, jj, r);
+  };
+  // MFMA i (< 16) of fragment set f: W block i / 4, X block i % 4.
+  auto mfma_one = [&](int f, int i) {
+    const int wb = i >> 2, b = i & 3;
+    acc[wb][b] = kRowLanes ? Mfma32(fw[f][wb], fx[f][b], acc[wb][b])
+                           : Mfma32(fx[f][b], fw[f][wb], acc[wb][b]);
+  };
+
+  // Prologue: DMAs of half-steps 0 .. 3 (indices past the last clamped:
+  // in-bounds reloads never read, so every half-step issues the same DMA
+  // count and the wait counts below are fixed), then half-step 0's first
+  // fragments once its DMAs have landed everywhere.
+  const int last = halves - 1;
+  dma(0, 0);
+  dma(1, min(1, last));
+  dma(2, min(2, last));
+  dma(3, min(3, last));
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(3 * kBigDmas) : "memory");
+  read_frag(0, 0, 0);
+
+  // Half-step s, ring slot s % 4: the 16 MFMAs of its first substep
+  // (fragments in registers), each followed by one of the reads of its
+  // second substep; then a barrier that waits for this wave's DMAs of
+  // half-step s + 1 and its LDS reads, after which half-step s + 1 is
+  // readable everywhere and slot s % 4 is read by no one; then the 16 MFMAs
+  // of the second substep, each followed by one of the DMAs of half-step
+  // s + 4 into slot s % 4 or one of the reads of half-step s + 1's first
+  // substep. With one wave per SIMD an MFMA holds up the wave's next
+  // instruction for its 32 clocks, so a memory instruction slotted between
+  // two MFMAs issues in that shadow; issued in a burst, the DMAs would stall
+  // the wave on a full memory queue while the matrix core idles.
+  auto half_step = [&](int s, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mfma_one(0, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i % 2 == 0)
+        read_one(1, slot, 1, i / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * kBigDmas) : "memory");
+    const int next = min(s + 4, last);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mfma_one(1, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i % 2 == 0)
+        dma_one(slot, next, i / 2);
+      else
+        read_one(0, (slot + 1) & 3, 0, i / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  int s = 0;
+  for (; s + 4 <= halves; s += 4) {
+    half_step(s, I0{});
+    half_step(s + 1, I1{});
+    half_step(s + 2, I2{});
+    half_step(s + 3, I3{});
+  }
+  if (s < halves) {  // halves is even: two more
+    half_step(s, I0{});
+    half_step(s + 1, I1{});
+  }
+  // No DMA may land in LDS once the epilogue uses it.
+  WaitLoads<0>();
+  __syncthreads();
+
+  WaveEpilogue<XB, WB, EPI>(p, acc, m0 + 128 * wr, split, tile_n * 8 + 4 * wc, wave, lane, lds);
+}
+
 // Packs row-major fp16 W [rows][K] into the fragment order above: half8
 // number ((block K/64 + t) 4 + j) 64 + l holds W[row(block, l % 32)][64 t +
 // 32 (l / 32) + 8 j .. + 7]; rows past `rows` are zero. One thread per half8.
@@ -659,7 +869,25 @@ void LaunchPackedWide(const GemmParams& p, const PackedPlan& plan, hipStream_t s
 }
 
 template <Epilogue EPI>
+void LaunchPackedBig(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  const int tiles_m = (p.m + 255) / 256;
+  const int tiles_n = (p.n + 255) / 256;
+  const int groups = tiles_m * tiles_n * p.splits;
+  Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
+  // The DMA offsets are 32-bit.
+  Require((static_cast<size_t>(p.m) * p.lda + p.k) * 2 < (size_t{1} << 31) &&
+              static_cast<size_t>(p.k / 64) * 2 * 4096 < (size_t{1} << 31),
+          "gemm: operands too large for the 256 x 256 tile");
+  Dispatch(PackedBigKernel<EPI>, dim3(groups), dim3(256), kBigLds, stream, true, true, p,
+           tiles_m, p.k / 64);
+}
+
+template <Epilogue EPI>
 void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  if (plan.xb == 8) {
+    LaunchPackedBig<EPI>(p, plan, stream);
+    return;
+  }
   if (plan.wb == 2) {
     LaunchPackedWide<EPI>(p, plan, stream);
     return;
@@ -709,11 +937,20 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   // round (fewer work-groups at once run faster each, but a few stragglers
   // still cost most of a round: the 10 s audio heads run 20.4 us as 390
   // 96-row tiles, 1.5 rounds, against 23.1 us as 132 wide tiles).
+  // The 256 x 256 tile (xb 8, wb 2) is priced by measurement instead: with
+  // every CU busy a K step takes it 1.45 times as long as the 128 x 256
+  // tile's (q/k/v at 3440 rows: 26.5 us of K loop in one round against
+  // 36.6 us in 1.7 rounds of the 128 x 256 tile), i.e. 1500 of these clocks.
   struct Shape {
     int xb, wb;
   };
   double best = 0.0;
-  for (const Shape sh : {Shape{4, 2}, Shape{4, 1}, Shape{3, 1}, Shape{2, 1}, Shape{1, 1}}) {
+  for (const Shape sh :
+       {Shape{8, 2}, Shape{4, 2}, Shape{4, 1}, Shape{3, 1}, Shape{2, 1}, Shape{1, 1}}) {
+    // The 256 x 256 tile's DMA offsets are 32-bit (X of the generator's
+    // GEMMs is [m][k]).
+    if (sh.xb == 8 && static_cast<size_t>(m) * k * 2 >= (size_t{1} << 31))
+      continue;
     const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) *
                       ((n + 128 * sh.wb - 1) / (128 * sh.wb)) * plan.splits;
     const int full = tiles / kCus, rest = tiles % kCus;
@@ -723,8 +960,8 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
     const double l2 = (32.0 * sh.xb + 128.0 * sh.wb) * 128.0 / 64.0;
     const double lds = 5.0 * 32.0 * sh.xb * 128.0 / 128.0;
     const double mfma = 4.0 * sh.xb * sh.wb * 32.0;
-    const double cost =
-        rounds * (static_cast<double>(steps) * std::max(l2, std::max(lds, mfma)) + 3200.0);
+    const double step = sh.xb == 8 ? 1500.0 : std::max(l2, std::max(lds, mfma));
+    const double cost = rounds * (static_cast<double>(steps) * step + 3200.0);
     if (best == 0.0 || cost < best) {
       best = cost;
       plan.xb = sh.xb;
@@ -742,8 +979,9 @@ void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue
   Require(p.splits == plan.splits && (p.k / 64) % p.splits == 0,
           "gemm: K steps not divisible by the split count");
   Require(p.lda % 8 == 0, "gemm: the row stride of X must be a multiple of 8");
-  Require(plan.xb >= 1 && plan.xb <= 4 && (plan.wb == 1 || (plan.wb == 2 && plan.xb == 4)),
-          "gemm: tile of 32 to 128 rows x 128 columns, or 128 x 256");
+  Require((plan.xb >= 1 && plan.xb <= 4 && (plan.wb == 1 || (plan.wb == 2 && plan.xb == 4))) ||
+              (plan.xb == 8 && plan.wb == 2),
+          "gemm: tile of 32 to 128 rows x 128 columns, 128 x 256 or 256 x 256");
   switch (epilogue) {
     case Epilogue::kStore:
     case Epilogue::kAccumulate:

@@ -128,11 +128,13 @@ def test_linear_matches_float64(rows, k, n, acc):
 @pytest.mark.parametrize("rows,k,n,acc", [
     (120, 1024, 4096, False), (580, 2048, 1024, True), (33, 512, 256, False),
     (500, 1024, 8200, False), (96, 384, 256, True), (1, 256, 128, False),
-    (3440, 1024, 6144, False), (85, 256, 1024, False)])
+    (3440, 1024, 6144, False), (85, 256, 1024, False), (300, 64, 384, True),
+    (700, 704, 768, False)])
 def test_packed_linear_matches_float64_at_every_tile(rows, k, n, acc):
     """The generator's packed-weight kernel against float64, at every tile
     shape, and bit-identical across shapes (a row's result does not depend
-    on the tile the packed row count selects)."""
+    on the tile the packed row count selects). K = 64 and 704 leave the
+    256 x 256 tile's half-step ring a remainder of two."""
     rng = np.random.default_rng(rows + n + 7)
     x = rng.standard_normal((rows, k)).astype(np.float16)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
@@ -142,7 +144,7 @@ def test_packed_linear_matches_float64_at_every_tile(rows, k, n, acc):
         want += y0
     scale = np.sqrt(k) * 0.02
     results = []
-    for tile in ((0, 0), (32, 128), (64, 128), (96, 128), (128, 128), (128, 256)):
+    for tile in ((0, 0), (32, 128), (64, 128), (96, 128), (128, 128), (128, 256), (256, 256)):
         y = dev(y0)
         ov.op_linear_packed(dev(x), dev(w), y, accumulate=acc, tile_rows=tile[0],
                             tile_cols=tile[1])

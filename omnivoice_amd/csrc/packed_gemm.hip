@@ -73,6 +73,17 @@ struct Packed {
   static constexpr int kLds = 4 * kStageBytes;   // ring of four K steps
 };
 
+// q/k epilogue staging of one head: 32 XB rows of 256 bytes.
+template <int XB>
+constexpr int kHeadStage = 32 * XB * 256;
+// The 128 x 256 tile's LDS: its ring, or the epilogue's sums ([4][128]
+// floats) and two heads' staging after them.
+constexpr int kWideSums = 4 * 128 * 4;
+constexpr int kWideLds = Packed<4>::kLds > kWideSums + 2 * kHeadStage<4>
+                             ? Packed<4>::kLds
+                             : kWideSums + 2 * kHeadStage<4>;
+static_assert(512 * 4 + kHeadStage<4> <= Packed<4>::kLds, "narrow q/k staging");
+
 // 16-byte chunk c of LDS row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1);
 // its own inverse.
 __device__ __forceinline__ int Swizzle(int row, int chunk) {
@@ -106,12 +117,15 @@ __host__ __device__ __forceinline__ int QkvHead(int slot, int total, int group) 
 
 // Epilogue of one wave: its WB packed 32-column blocks block0 .. block0 +
 // WB - 1 (consecutive, inside one tile), accumulators acc[wb][b] for the
-// tile's 32-row blocks b. Every result is rounded the same way whatever XB
-// and WB are, so a row's outputs do not depend on the tile shape.
+// 32-row blocks b of rows m0 ... Every result is rounded the same way
+// whatever XB and WB are, so a row's outputs do not depend on the tile
+// shape. `stage`: LDS offset of the q/k staging rows of this wave's head
+// (32 XB rows of 256 bytes, shared by the 4 / WB waves of the head, clear of
+// the LDS sums below).
 template <int XB, int WB, Epilogue EPI>
 __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc)[WB][XB],
                                              int m0, int split, int block0, int wave,
-                                             int lane, unsigned char* lds) {
+                                             int lane, unsigned char* lds, int stage) {
   constexpr int kBM = 32 * XB;
   const int h = lane >> 5;
   const int col = lane & 31;
@@ -174,6 +188,36 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
     const int total = p.heads + 2 * p.kv_heads;
     const int slot = QkvHead(block0 / 4, total, p.heads / p.kv_heads);
     const bool qk = live && slot >= 0 && slot < p.heads + p.kv_heads;
+    const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
+    // The rotary rows and norm weights of block wb (this lane's rotary
+    // indices c = 16 (block % 4) + 8 g + 4 h + i, g < 2, i < 4), loaded a
+    // block ahead into one of two register sets; the first block's before
+    // the sums, so that their latency overlaps the sums and the barrier
+    // rather than stalling once per block. Rows past M read row M - 1.
+    float2 rot[2][XB][8];
+    float wt[2][16];  // w_lo[g][i] at 4 g + i, w_hi at 8 + 4 g + i
+    auto load_rope = [&](int buf, int wb) {
+      const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wt[buf][4 * g + i] = weight[c_base + 8 * g + i];
+          wt[buf][8 + 4 * g + i] = weight[64 + c_base + 8 * g + i];
+        }
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int m = min(m0 + 32 * b + col, p.m - 1);
+        const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            rot[buf][b][4 * g + i] = cs[8 * g + i];
+      }
+    };
+    if (qk)
+      load_rope(0, 0);
     // Sum of squares of each block's 32 columns of a row, then over the
     // head's four blocks in the fixed order (0 + 1) + (2 + 3): a wave adds
     // its own pair when it holds two blocks, or all four when it holds the
@@ -198,11 +242,14 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           sums[wave * kBM + 32 * b + col] = WB == 2 ? part[0][b] + part[WB - 1][b] : part[0][b];
       }
     }
-    __syncthreads();
+    Barrier();  // LDS only: the rotary loads stay in flight
+    // q/k heads: normalised and rotated values go to this head's LDS
+    // staging rows (32 XB rows of 256 bytes at `stage`, 16-byte chunk c of
+    // row r at position c ^ (r % 16)), from which the waves that share the
+    // head store whole rows with 16-byte stores below (written straight
+    // from the MFMA layout, a store would cover 32 rows of 16 bytes each).
     if (qk) {
-      const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
-      // The first of the waves that hold this head.
-      const int first = WB == 2 ? (wave & ~1) : 0;
+      const int first = WB == 2 ? (wave & ~1) : 0;  // the first wave of this head
       float scale[XB];
 #pragma unroll
       for (int b = 0; b < XB; ++b) {
@@ -219,36 +266,27 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
       }
 #pragma unroll
       for (int wb = 0; wb < WB; ++wb) {
-        // This lane's rotary indices: c = 16 (block % 4) + 8 g + 4 h + i, g < 2.
-        const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
-        float w_lo[2][4], w_hi[2][4];
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            w_lo[g][i] = weight[c_base + 8 * g + i];
-            w_hi[g][i] = weight[64 + c_base + 8 * g + i];
-          }
+        if (wb + 1 < WB)
+          load_rope((wb + 1) & 1, wb + 1);
+        const int f = wb & 1;
+        const int chunk0 = 2 * ((block0 + wb) & 3);  // chunks chunk0 + g, chunk0 + 8 + g
 #pragma unroll
         for (int b = 0; b < XB; ++b) {
-          const int m = m0 + 32 * b + col;
-          if (m >= p.m)
-            continue;
-          const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
-          half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + c_base;
+          const int r_local = 32 * b + col;
+          unsigned char* row = lds + stage + r_local * 256 + 8 * h;
 #pragma unroll
           for (int g = 0; g < 2; ++g) {
             half4 lo, hi;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float2 rot = cs[8 * g + i];
-              const float a = w_lo[g][i] * (acc[wb][b][4 * g + i] * scale[b]);
-              const float bb = w_hi[g][i] * (acc[wb][b][4 * g + 8 + i] * scale[b]);
-              lo[i] = static_cast<half_t>(__builtin_fmaf(a, rot.x, -(bb * rot.y)));
-              hi[i] = static_cast<half_t>(__builtin_fmaf(bb, rot.x, a * rot.y));
+              const float2 cs = rot[f][b][4 * g + i];
+              const float a = wt[f][4 * g + i] * (acc[wb][b][4 * g + i] * scale[b]);
+              const float bb = wt[f][8 + 4 * g + i] * (acc[wb][b][4 * g + 8 + i] * scale[b]);
+              lo[i] = static_cast<half_t>(__builtin_fmaf(a, cs.x, -(bb * cs.y)));
+              hi[i] = static_cast<half_t>(__builtin_fmaf(bb, cs.x, a * cs.y));
             }
-            *reinterpret_cast<half4*>(out + 8 * g) = lo;
-            *reinterpret_cast<half4*>(out + 64 + 8 * g) = hi;
+            *reinterpret_cast<half4*>(row + (((chunk0 + g) ^ (r_local & 15)) << 4)) = lo;
+            *reinterpret_cast<half4*>(row + (((chunk0 + 8 + g) ^ (r_local & 15)) << 4)) = hi;
           }
         }
       }
@@ -272,6 +310,24 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
                 static_cast<half_t>(acc[wb][b][r]);
           }
         }
+      }
+    }
+    Barrier();
+    if (qk) {
+      // The 4 / WB waves of this head copy its staged rows out, 16 lanes per
+      // 256-byte row.
+      constexpr int kGroup = 4 / WB;
+      constexpr int kRowsPerPass = 4 * kGroup;
+      const int t = (wave % kGroup) * 64 + lane;
+      const int q = t & 15;
+#pragma unroll
+      for (int pass = 0; pass < 32 * XB / kRowsPerPass; ++pass) {
+        const int r = pass * kRowsPerPass + (t >> 4);
+        const int m = m0 + r;
+        const half8 v =
+            *reinterpret_cast<const half8*>(lds + stage + r * 256 + ((q ^ (r & 15)) << 4));
+        if (m < p.m)
+          *reinterpret_cast<half8*>(p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + 8 * q) = v;
       }
     }
   }
@@ -444,7 +500,8 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   if (whole + 2 < steps)
     step(whole + 2, I2{});
 
-  WaveEpilogue<XB, 1, EPI>(p, acc, m0, split, block, wave, lane, lds);
+  // q/k staging after the LDS sums ([4][32 XB] floats).
+  WaveEpilogue<XB, 1, EPI>(p, acc, m0, split, block, wave, lane, lds, 512 * XB);
 }
 
 // The wide tile for large M: 128 x 256, each wave owning two packed blocks
@@ -606,7 +663,9 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   if (whole + 2 < steps)
     step(whole + 2, I2{});
 
-  WaveEpilogue<XB, WB, EPI>(p, acc, m0, split, block0, wave, lane, lds);
+  // Two heads' q/k staging (waves 0-1, 2-3) after the LDS sums.
+  WaveEpilogue<XB, WB, EPI>(p, acc, m0, split, block0, wave, lane, lds,
+                            kWideSums + (wave >> 1) * kHeadStage<XB>);
 }
 
 // The large tile for large M: 256 x 256, four waves in a 2 x 2 arrangement,
@@ -627,6 +686,7 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
 constexpr int kBigHalf = 32768;         // one half-step: X 16 KB, then W 16 KB
 constexpr int kBigLds = 4 * kBigHalf;   // ring of four half-steps
 constexpr int kBigDmas = 8;             // DMAs per wave per half-step
+static_assert(4 * kHeadStage<4> <= kBigLds, "q/k staging of four heads in the ring");
 
 // Position of chunk q of 64-byte LDS row r: distinct banks for the rows of
 // a fragment read in both 8-lane (128-byte) and 16-lane (256-byte) phases.
@@ -812,7 +872,9 @@ void PackedBigKernel(GemmParams p, int tiles_m, int k_steps) {
   WaitLoads<0>();
   __syncthreads();
 
-  WaveEpilogue<XB, WB, EPI>(p, acc, m0 + 128 * wr, split, tile_n * 8 + 4 * wc, wave, lane, lds);
+  // Each wave's head staged in its own quarter of the ring.
+  WaveEpilogue<XB, WB, EPI>(p, acc, m0 + 128 * wr, split, tile_n * 8 + 4 * wc, wave, lane, lds,
+                            wave * kHeadStage<XB>);
 }
 
 // Packs row-major fp16 W [rows][K] into the fragment order above: half8
@@ -864,8 +926,8 @@ void LaunchPackedWide(const GemmParams& p, const PackedPlan& plan, hipStream_t s
   const int tiles_n = (p.n + 255) / 256;
   const int groups = tiles_m * tiles_n * p.splits;
   Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
-  Dispatch(PackedWideKernel<EPI>, dim3(groups), dim3(256), Packed<4>::kLds, stream, true, true,
-           p, tiles_m, p.k / 64);
+  Dispatch(PackedWideKernel<EPI>, dim3(groups), dim3(256), kWideLds, stream, true, true, p,
+           tiles_m, p.k / 64);
 }
 
 template <Epilogue EPI>

@@ -452,32 +452,40 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   for (int j = 0; j < 4; ++j)
     read_frag(fr[0][j], 0, j);
 
-  // Step t (LDS buffers by t % 4, register slots by t % 4 and t % 2): write
-  // X(t + 2) into buffer (t + 2) % 4 (its previous content, X(t - 2), was
-  // last read in step t - 3) and reload those registers with X(t + 4); run
-  // the 16 MFMAs of step t from fragments already in registers while reading
-  // X(t + 1)'s fragments from buffer (t + 1) % 4 (written in step t - 1,
-  // before the barrier that ended it), so no MFMA waits for LDS; reload W's
-  // slot with W(t + 4); end at a barrier that first waits for all of the
-  // step's LDS operations, after which X(t + 2) is readable. (Letting the
-  // fragment reads run on across the barrier measured no faster.)
+  // Step t (LDS buffers by t % 4, register slots by t % 4 and t % 2): the
+  // 4 XB MFMAs of step t from fragments already in registers, each followed
+  // by memory work of the step, so that it issues in the MFMA's shadow (with
+  // one wave per SIMD an MFMA holds up the wave's next instruction for its 32
+  // clocks): first, one per row block, the write of X(t + 2) into buffer
+  // (t + 2) % 4 (its previous content, X(t - 2), was last read in step
+  // t - 3) and the reload of those registers with X(t + 4); after every
+  // MFMA one read of X(t + 1)'s fragments from buffer (t + 1) % 4 (written in
+  // step t - 1, before the barrier that ended it), so no MFMA waits for LDS;
+  // after a substep's last MFMA the reload of its W slot with W(t + 4). The
+  // step ends at a barrier that first waits for all of its LDS operations,
+  // after which X(t + 2) is readable. (Letting the fragment reads run on
+  // across the barrier measured no faster.)
   auto step = [&](int t, auto slot) {
     constexpr int ws = decltype(slot)::value;  // t % 4
     constexpr int xo = ws & 1;                 // t % 2
-    store_x(xs[xo], (ws + 2) & 3);
-    AsmFence();
-    load_x(xs[xo], min(t + 4, last));
+    const int ahead = min(t + 4, last);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      read_frag(fr[1 - xo][j], (ws + 1) & 3, j);
+    for (int i = 0; i < 4 * XB; ++i) {
+      const int j = i / XB, b = i % XB;
+      acc[0][b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[0][b])
+                            : Mfma32(fr[xo][j][b], wf[ws][j], acc[0][b]);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int b = 0; b < XB; ++b)
-        acc[0][b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[0][b])
-                              : Mfma32(fr[xo][j][b], wf[ws][j], acc[0][b]);
+      if (i < XB) {
+        *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[i]) = xs[xo][i];
+        AsmFence();
+        xs[xo][i] = x_src[i][ahead * 8];
+      }
+      fr[1 - xo][i / XB][i % XB] = *reinterpret_cast<const half8*>(
+          lds + ((ws + 1) & 3) * S::kStageBytes + x_read[i % XB][i / XB]);
+      if (b == XB - 1)
+        wf[ws][j] = w_src[(ahead * 4 + j) * 64];
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_w(wf[ws], min(t + 4, last));
     Barrier();
   };
   using I0 = std::integral_constant<int, 0>;
@@ -614,35 +622,47 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   Barrier();
   read_frag(fr[0], 0, 0);
 
-  // Step t: write X(t + 2) into LDS buffer (t + 2) % 4 and reload those
-  // registers with X(t + 4); for each substep j run its eight MFMAs from
-  // fragments in registers after issuing the reads of the next substep
-  // (substep j + 1 of buffer t % 4, or the first substep of step t + 1 from
-  // buffer (t + 1) % 4, written in step t - 1); reload W's slot with
-  // W(t + 2); end at a barrier that waits for all of the step's LDS
-  // operations. A buffer is rewritten two barriers after its last read.
+  // Step t: for each substep j its eight MFMAs from fragments in
+  // registers, each followed by memory work of the step, so that it issues
+  // in the MFMA's shadow (with one wave per SIMD an MFMA holds up the wave's
+  // next instruction for its 32 clocks): after every other MFMA one read of
+  // the next substep's fragments (substep j + 1 of buffer t % 4, or the
+  // first substep of step t + 1 from buffer (t + 1) % 4, written in step
+  // t - 1); in substep 0, after the others, the write of X(t + 2) into LDS
+  // buffer (t + 2) % 4 and the reload of those registers with X(t + 4);
+  // after the last MFMA of a W fragment its reload with W(t + 2). The step
+  // ends at a barrier that waits for all of its LDS operations. A buffer is
+  // rewritten two barriers after its last read.
   auto step = [&](int t, auto slot) {
     constexpr int ws = decltype(slot)::value;  // t % 4
     constexpr int xo = ws & 1;                 // t % 2
-    store_x(xs[xo], (ws + 2) & 3);
-    AsmFence();
-    load_x(xs[xo], min(t + 4, last));
+    const int ahead_x = min(t + 4, last);
+    const int ahead_w = min(t + 2, last);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < 3)
-        read_frag(fr[(j + 1) & 1], ws, j + 1);
-      else
-        read_frag(fr[0], (ws + 1) & 3, 0);
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int wb = 0; wb < WB; ++wb)
-#pragma unroll
-        for (int b = 0; b < XB; ++b)
-          acc[wb][b] = kRowLanes ? Mfma32(wf[xo][wb][j], fr[j & 1][b], acc[wb][b])
-                                 : Mfma32(fr[j & 1][b], wf[xo][wb][j], acc[wb][b]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < WB * XB; ++i) {
+        const int wb = i / XB, b = i % XB;
+        acc[wb][b] = kRowLanes ? Mfma32(wf[xo][wb][j], fr[j & 1][b], acc[wb][b])
+                               : Mfma32(fr[j & 1][b], wf[xo][wb][j], acc[wb][b]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i % 2 == 0) {
+          const int rb = i / 2;
+          const int buf = j < 3 ? ws : (ws + 1) & 3;
+          fr[(j + 1) & 1][rb] = *reinterpret_cast<const half8*>(
+              lds + buf * S::kStageBytes + x_read[rb][j < 3 ? j + 1 : 0]);
+        } else if (j == 0) {
+          const int xi = i / 2;
+          *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) =
+              xs[xo][xi];
+          AsmFence();
+          xs[xo][xi] = x_src[xi][ahead_x * 8];
+        }
+        if (b == XB - 1)
+          wf[xo][wb][j] = w_src[wb * w_next + (ahead_w * 4 + j) * 64];
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    load_w(wf[xo], min(t + 2, last));
     Barrier();
   };
   using I0 = std::integral_constant<int, 0>;

@@ -297,6 +297,25 @@ def gemm_compare(args, torch):
                       "torch": torch.__version__, "rows": out}), flush=True)
 
 
+def linear_tiles(specs, torch):
+    """Five launches of the packed-weight GEMM per shape with the tile
+    forced (fp32 stores, seeded fp16 operands), nothing timed: a fixed
+    workload for rocprofv3 counter passes over one kernel kind each."""
+    import omnivoice_amd as ov
+    rng = np.random.default_rng(0)
+    for spec in specs:
+        shape, tile = spec.split(":")
+        m, n, k = (int(v) for v in shape.split("x"))
+        r, c = (int(v) for v in tile.split("x"))
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float16)).cuda()
+        w = torch.from_numpy((rng.standard_normal((n, k)) * 0.02).astype(np.float16)).cuda()
+        y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        for _ in range(5):
+            ov.op_linear_packed(x, w, y, tile_rows=r, tile_cols=c)
+        torch.cuda.synchronize()
+        print(json.dumps({"linear": spec, "launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -315,6 +334,10 @@ def main():
                     help="benchmark the audio encoder on the workload's length of audio")
     ap.add_argument("--gemm-compare", action="store_true",
                     help="time the vendor GEMM (torch.matmul) at the backbone's shapes")
+    ap.add_argument("--linear-tiles", nargs="*", default=None, metavar="MxNxK:RxC",
+                    help="only run ovg_op_linear_packed five times per shape with the "
+                         "tile forced (e.g. 3440x4096x1024:256x256), for counter "
+                         "passes, and exit")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only copy this many MiB device to device 3 times (a "
                          "copy kernel of known size for calibrating memory "
@@ -336,6 +359,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": n, "copies": 3}), flush=True)
+        return
+    if args.linear_tiles is not None:
+        linear_tiles(args.linear_tiles, torch)
         return
     if args.codec:
         bench_codec(args, torch)

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 
 namespace ovg {
@@ -17,15 +18,25 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kWave = 64;
 
 // Each packed sequence starts at a multiple of this many rows, so that its
-// 32-key tiles of V^T start on whole 16-row blocks (see VtColumn).
+// 32-key tiles of V^T are two whole 16-row blocks (see VtIndex).
 constexpr int kSequenceAlign = 16;
 
-// Column of packed row `row` in V^T ([kv head][dim][column]): within every
-// 16-row block the rows are stored in the order 0-3, 8-11, 4-7, 12-15, the
-// key order of the attention kernel's probability operand.
+// Column of packed row `row` in V^T: within every 16-row block the rows are
+// stored in the order 0-3, 8-11, 4-7, 12-15, the key order of the attention
+// kernel's probability operand.
 __host__ __device__ constexpr int VtColumn(int row) {
   return (row & ~15) | (((row >> 2) & 1) << 3) | (((row >> 3) & 1) << 2) |
          (row & 3);
+}
+
+// V^T layout: per kv head, `ldvt` rows (a multiple of 16) in blocks of 16
+// rows; block b is [128 dims][16 rows] fp16 (4 KB), the rows in VtColumn
+// order. A 32-key tile that starts on a 16-row boundary is then 8 KB of
+// consecutive bytes, which the attention fetches as whole cache lines.
+// Element index of (kv head g, dim d, packed row `row`):
+__host__ __device__ constexpr std::size_t VtIndex(int g, int d, int row, int ldvt) {
+  return (static_cast<std::size_t>(g) * 128 * ldvt) +
+         static_cast<std::size_t>(row >> 4) * 2048 + d * 16 + (VtColumn(row) & 15);
 }
 
 // Output stores that write through to memory: relaxed device-scope atomic

@@ -1,7 +1,8 @@
-// fp16 x fp16 -> fp32 GEMM on gfx950 matrix cores with the generator's
-// epilogues fused (replaces the hipBLASLt calls of the reference's
-// HalfGemm::Linear, gemm.cpp:248-262, and the QkNormRope / SwiGlu kernels
-// that followed them, kernels/generator_kernels.hip:102-159, 191-200).
+// fp16 x fp16 -> fp32 GEMM on gfx950 matrix cores over unpacked row-major
+// weights: the stand-alone linear operator (ovg_op_linear and its
+// allocation-free variant), the reference's HalfGemm::Linear (gemm.cpp:
+// 248-262). The generator's own projections, with their fused q/k/v and
+// SwiGLU epilogues, run on weights packed at load (packed_gemm.hip).
 //
 // Y[m][n] = sum_k X[m][k] W[n][k]: both operands are K-contiguous, so a
 // lane's eight consecutive k values are one 16-byte fragment of a
@@ -23,12 +24,7 @@
 // (16-byte per lane, conflict-free) so that each wave ends up owning 16 rows
 // x 128 columns of the summed tile (group 0 + group 1; fp32 addition of two
 // terms is commutative, so both owners round identically), and writes them
-// straight from registers: plain or residual-accumulating fp32 stores; the
-// q/k/v epilogue (per-head RMSNorm is a 32-lane reduction, rotate-half pairs
-// are columns c and c + 64 of the same lane, value heads are written
-// transposed, four consecutive rows per 8-byte store); or SwiGLU over the
-// interleaved gate/up weight tile (columns c and c + 64 are the gate and up
-// of one output).
+// straight from registers: plain or residual-accumulating fp32 stores.
 //
 // Split-K: with the kPartial epilogue every split stores its own fp32 slice
 // and the row kernel that consumes the output sums the slices; the split
@@ -120,16 +116,6 @@ __device__ __forceinline__ int RowOf(int e, int lane) {
   return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
 }
 
-// Sum over the 32 lanes that share lane >> 5: DPP within 16-lane rows, then
-// the two rows of each half.
-__device__ __forceinline__ float HalfWaveSum(float v) {
-  v = DppAdd<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = DppAdd<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = DppAdd<0x141>(v);  // row_half_mirror
-  v = DppAdd<0x140>(v);  // row_mirror
-  return v + __shfl_xor(v, 16);
-}
-
 // Partial slices are stored write-through (their lines would otherwise keep
 // the kernel alive at its end while L2 writes them back; the row kernel that
 // sums them reads them from memory either way). Final outputs are stored
@@ -160,94 +146,6 @@ __device__ __forceinline__ void StoreOwned(const GemmParams& p,
   }
 }
 
-template <int FM>
-__device__ __forceinline__ void QkvOwned(const GemmParams& p,
-                                         const Owned<FM>& o, int row0,
-                                         int slot) {
-  const int lane = threadIdx.x & 63;
-  const int j = lane & 31;
-  if (slot < p.heads + p.kv_heads) {
-    const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
-    float w[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      w[c] = weight[32 * c + j];
-    // Every rotary load is issued before the arithmetic (one memory round
-    // trip: the table is already gathered per packed row).
-    float2 cs[8 * FM][2];
-#pragma unroll
-    for (int e = 0; e < 8 * FM; ++e)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-        cs[e][c] = p.rope[static_cast<size_t>(min(row0 + RowOf(e, lane), p.m - 1)) * 64 +
-                          32 * c + j];
-#pragma unroll
-    for (int e = 0; e < 8 * FM; ++e) {
-      const int m = row0 + RowOf(e, lane);
-      float squares = o.v[0][e] * o.v[0][e];
-#pragma unroll
-      for (int c = 1; c < 4; ++c)
-        squares = __builtin_fmaf(o.v[c][e], o.v[c][e], squares);
-      squares = HalfWaveSum(squares);
-      const float scale = rsqrtf(__builtin_fmaf(squares, 1.0F / 128.0F, p.eps));
-      if (m >= p.m)
-        continue;
-      half_t* out = p.qk + static_cast<size_t>(m) * p.ldq + slot * 128;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const float a = w[c] * (o.v[c][e] * scale);
-        const float b = w[c + 2] * (o.v[c + 2][e] * scale);
-        out[32 * c + j] = static_cast<half_t>(__builtin_fmaf(a, cs[e][c].x, -(b * cs[e][c].y)));
-        out[32 * c + j + 64] =
-            static_cast<half_t>(__builtin_fmaf(b, cs[e][c].x, a * cs[e][c].y));
-      }
-    }
-    return;
-  }
-  // Value heads: V^T[g][d][VtColumn(row)]; e = 4 h .. 4 h + 3 are four
-  // consecutive rows starting at a multiple of 4, which VtColumn keeps
-  // consecutive.
-  const int g = slot - p.heads - p.kv_heads;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    half_t* out = p.vt + static_cast<size_t>(g * 128 + 32 * c + j) * p.ldvt;
-#pragma unroll
-    for (int h = 0; h < 2 * FM; ++h) {
-      const int m = row0 + RowOf(4 * h, lane);
-      const half4 v = {static_cast<half_t>(o.v[c][4 * h]),
-                       static_cast<half_t>(o.v[c][4 * h + 1]),
-                       static_cast<half_t>(o.v[c][4 * h + 2]),
-                       static_cast<half_t>(o.v[c][4 * h + 3])};
-      if (m + 3 < p.m) {
-        *reinterpret_cast<half4*>(out + VtColumn(m)) = v;
-      } else {
-        for (int e = 0; e < 4 && m + e < p.m; ++e)
-          out[VtColumn(m + e)] = v[e];
-      }
-    }
-  }
-}
-
-template <int FM>
-__device__ __forceinline__ void SwiGluOwned(const GemmParams& p,
-                                            const Owned<FM>& o, int row0,
-                                            int tile_n) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int e = 0; e < 8 * FM; ++e) {
-    const int m = row0 + RowOf(e, lane);
-    if (m >= p.m)
-      continue;
-    half_t* out = p.act + static_cast<size_t>(m) * p.ldh + tile_n * 64 + (lane & 31);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const float g = o.v[c][e];
-      const float u = o.v[c + 2][e];
-      out[32 * c] = static_cast<half_t>(g / (1.0F + __expf(-g)) * u);
-    }
-  }
-}
-
 template <Epilogue EPI, int FM>
 __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
                                               const Owned<FM>& o, int row0,
@@ -256,10 +154,6 @@ __device__ __forceinline__ void OwnedEpilogue(const GemmParams& p,
     StoreOwned<FM, false>(p, o, p.y, row0, tile_n * kBN, false);
   else if constexpr (EPI == Epilogue::kAccumulate)
     StoreOwned<FM, false>(p, o, p.y, row0, tile_n * kBN, true);
-  else if constexpr (EPI == Epilogue::kQkvRope)
-    QkvOwned(p, o, row0, tile_n);
-  else if constexpr (EPI == Epilogue::kSwiGlu)
-    SwiGluOwned(p, o, row0, tile_n);
 }
 
 // ------------------------------------------------------------- main kernel
@@ -753,15 +647,8 @@ void LaunchGemm(const GemmParams& p, const GemmPlan& plan, Epilogue epilogue,
       LaunchEpi<Epilogue::kAccumulate>(p, plan, stream);
       break;
     case Epilogue::kQkvRope:
-      Require(p.n == (p.heads + 2 * p.kv_heads) * 128,
-              "gemm: q/k/v epilogue needs N = (heads + 2 kv_heads) * 128");
-      Require(p.ldvt % 16 == 0, "gemm: V^T rows must hold whole 16-row blocks");
-      LaunchEpi<Epilogue::kQkvRope>(p, plan, stream);
-      break;
     case Epilogue::kSwiGlu:
-      Require(p.n % 128 == 0, "gemm: SwiGLU epilogue needs N % 128 == 0");
-      LaunchEpi<Epilogue::kSwiGlu>(p, plan, stream);
-      break;
+      throw Error("gemm: the q/k/v and SwiGLU epilogues run on packed weights (LaunchPacked)");
     case Epilogue::kPartial:
       Require(p.y != nullptr &&
                   p.split_stride >= static_cast<std::size_t>(p.m) * p.ldc,

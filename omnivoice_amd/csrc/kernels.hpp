@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "common.hpp"
 
@@ -63,7 +64,8 @@ enum class Epilogue : int {
   kStore = 0,       // y fp32 [M][ldc] = acc
   kAccumulate = 1,  // y fp32 [M][ldc] += acc (the residual stream)
   kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
-                    // qk [M][ldq]; v heads -> fp16 V^T
+                    // qk, head-major: element (head, row, d) at
+                    // head * ldq + row * 128 + d; v heads -> fp16 V^T
                     // vt[g][d][VtColumn(row)] (ldvt % 16 == 0)
   kSwiGlu = 3,      // act fp16 [M][ldh] = silu(gate) * up; the W rows pair
                     // gate and up rows: per 128-row tile 64 gate rows then
@@ -195,9 +197,12 @@ struct AddNormParams {
 };
 void LaunchAddNorm(const AddNormParams& p, hipStream_t stream);
 
-// vt[g][d][VtColumn(r)] = qkv[r][(heads + kv_heads + g) * 128 + d], r < rows.
-void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
-                      int rows, int heads, int kv_heads, hipStream_t stream);
+// The attention's operand layouts from row-major q|k|v rows (r < rows):
+// qk[h * ldq + r * 128 + d] = qkv[r][h * 128 + d] for the q and k heads,
+// vt[VtIndex(g, d, r, ldvt)] = qkv[r][(heads + kv_heads + g) * 128 + d].
+void LaunchAttentionLayout(const half_t* qkv, int ld_qkv, half_t* qk, int ldq,
+                           half_t* vt, int ldvt, int rows, int heads, int kv_heads,
+                           hipStream_t stream);
 
 void LaunchFill(int* data, int value, int count, hipStream_t stream);
 
@@ -211,7 +216,8 @@ struct AttentionWork {
   int q_begin, q_count, seq_begin, seq_length;
 };
 struct AttentionParams {
-  const half_t* qk;        // [rows][ld_qk]: q heads, then k heads
+  const half_t* qk;        // head-major: q heads then k heads, element
+                           // (head, row, d) at head * ld_qk + row * 128 + d
   const half_t* vt;        // [kv_heads][128][ldvt], columns by VtColumn
   half_t* out;             // [rows][heads * 128]
   const AttentionWork* work;
@@ -225,7 +231,18 @@ struct AttentionParams {
   const unsigned char* prefetch[kMaxPrefetch];
   unsigned long long prefetch_bytes[kMaxPrefetch];
   int prefetch_groups;
+  // work[0, exact_count): sequences of at most kExactAttentionKeys keys,
+  // whose scores fit in registers (two-pass softmax, at most exact_rounds
+  // rounds of four 32-key tiles); the rest take the online-softmax kernel.
+  int exact_count;
+  int exact_rounds;
 };
+constexpr int kExactAttentionKeys = 768;
+// Orders `work` so that the items of sequences of at most
+// kExactAttentionKeys keys come first (each group in its given order) and
+// sets AttentionParams::exact_count / exact_rounds for it. Which kernel a
+// query takes depends on its own sequence's length only.
+void PlanAttentionWork(std::vector<AttentionWork>& work, int* exact_count, int* exact_rounds);
 void LaunchAttention(const AttentionParams& p, hipStream_t stream);
 
 // ---------------------------------------------------------------- decoding

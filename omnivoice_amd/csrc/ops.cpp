@@ -242,38 +242,39 @@ int ovg_op_attention(const void* qkv, void* output, int64_t rows,
                         static_cast<int>(std::min<int64_t>(32, length - q)),
                         static_cast<int>(first), static_cast<int>(length)});
     }
+    int exact_count = 0, exact_rounds = 0;
+    ovg::PlanAttentionWork(work, &exact_count, &exact_rounds);
     auto s = static_cast<hipStream_t>(stream);
-    // Keys are read in whole 32-row tiles: copy q|k into a buffer padded to
-    // the last tile, and V into V^T.
+    // Keys are read in whole 32-row tiles: q and k go head-major into a
+    // buffer padded past the last tile, V into V^T blocks.
     const int padded = static_cast<int>(std::max(end, rows));
     const int ldvt = (padded + 15) / 16 * 16;
-    Scratch<ovg::half_t> qk(static_cast<std::size_t>(padded) * ld_qkv);
+    const int ldq = ldvt * 128;
+    Scratch<ovg::half_t> qk(static_cast<std::size_t>(heads + kv_heads) * ldq);
     Scratch<ovg::half_t> vt(static_cast<std::size_t>(kv_heads) * 128 * ldvt);
     Scratch<ovg::AttentionWork> dwork(work.size());
     ovg::Check(hipMemsetAsync(qk.data, 0,
-                              static_cast<std::size_t>(padded) * ld_qkv * 2, s),
+                              static_cast<std::size_t>(heads + kv_heads) * ldq * 2, s),
                "clear");
     ovg::Check(hipMemsetAsync(vt.data, 0,
                               static_cast<std::size_t>(kv_heads) * 128 * ldvt * 2, s),
                "clear");
-    ovg::Check(hipMemcpyAsync(qk.data, qkv,
-                              static_cast<std::size_t>(rows) * ld_qkv * 2,
-                              hipMemcpyDeviceToDevice, s),
-               "copy");
     ovg::Check(hipMemcpyAsync(dwork.data, work.data(),
                               work.size() * sizeof(ovg::AttentionWork),
                               hipMemcpyHostToDevice, s),
                "upload");
-    ovg::LaunchTransposeV(static_cast<const ovg::half_t*>(qkv), ld_qkv,
-                          vt.data, ldvt, static_cast<int>(rows),
-                          static_cast<int>(heads), static_cast<int>(kv_heads), s);
+    ovg::LaunchAttentionLayout(static_cast<const ovg::half_t*>(qkv), ld_qkv, qk.data, ldq,
+                               vt.data, ldvt, static_cast<int>(rows),
+                               static_cast<int>(heads), static_cast<int>(kv_heads), s);
     ovg::AttentionParams p{};
     p.qk = qk.data;
     p.vt = vt.data;
     p.out = static_cast<ovg::half_t*>(output);
     p.work = dwork.data;
     p.work_count = static_cast<int>(work.size());
-    p.ld_qk = ld_qkv;
+    p.exact_count = exact_count;
+    p.exact_rounds = exact_rounds;
+    p.ld_qk = ldq;
     p.ldvt = ldvt;
     p.heads = static_cast<int>(heads);
     p.kv_heads = static_cast<int>(kv_heads);

@@ -291,8 +291,8 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
         }
       }
     } else if (live && slot >= 0) {
-      // Value head gv: V^T[gv][d][VtColumn(row)], d the head column of the
-      // element (rope order inside the block).
+      // Value head gv: V^T element (gv, d, row) at VtIndex, d the head
+      // column of the element (rope order inside the block).
       const int gv = slot - p.heads - p.kv_heads;
 #pragma unroll
       for (int wb = 0; wb < WB; ++wb) {
@@ -302,12 +302,11 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           const int m = m0 + 32 * b + col;
           if (m >= p.m)
             continue;
-          const int column = VtColumn(m);
+          half_t* column = p.vt + VtIndex(gv, 0, m, p.ldvt);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
-            p.vt[static_cast<size_t>(gv * 128 + d) * p.ldvt + column] =
-                static_cast<half_t>(acc[wb][b][r]);
+            column[d * 16] = static_cast<half_t>(acc[wb][b][r]);
           }
         }
       }
@@ -327,7 +326,7 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
         const half8 v =
             *reinterpret_cast<const half8*>(lds + stage + r * 256 + ((q ^ (r & 15)) << 4));
         if (m < p.m)
-          *reinterpret_cast<half8*>(p.qk + static_cast<size_t>(m) * p.ldq + slot * 128 + 8 * q) = v;
+          *reinterpret_cast<half8*>(p.qk + static_cast<size_t>(slot) * p.ldq + m * 128 + 8 * q) = v;
       }
     }
   }
@@ -1081,7 +1080,9 @@ void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue
     case Epilogue::kQkvRope:
       Require(p.n == (p.heads + 2 * p.kv_heads) * 128,
               "gemm: q/k/v epilogue needs N = (heads + 2 kv_heads) * 128");
-      Require(p.ldvt % 16 == 0 && p.ldq % 4 == 0, "gemm: q/k/v output strides");
+      Require(p.ldvt % 16 == 0 && p.ldq % 128 == 0 &&
+                  static_cast<int64_t>(p.ldq) >= static_cast<int64_t>(p.m) * 128,
+              "gemm: q/k/v output strides");
       LaunchPackedEpi<Epilogue::kQkvRope>(p, plan, stream);
       break;
     case Epilogue::kSwiGlu:

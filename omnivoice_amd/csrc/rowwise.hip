@@ -294,16 +294,21 @@ __global__ __launch_bounds__(64) void AddNorm1024Kernel(AddNormParams p) {
               static_cast<half_t>(wv[i][3] * (v[i][3] * scale))};
 }
 
-// One thread per (kv head, dim, row).
-__global__ void TransposeVKernel(const half_t* qkv, int ld_qkv, half_t* vt,
-                                 int ldvt, int rows, int heads, int kv_heads) {
+// One thread per (head slot, dim, row): slots below heads + kv_heads are q
+// and k heads (head-major copy), the rest value heads (V^T blocks).
+__global__ void AttentionLayoutKernel(const half_t* qkv, int ld_qkv, half_t* qk, int ldq,
+                                      half_t* vt, int ldvt, int rows, int heads,
+                                      int kv_heads) {
   const int row = blockIdx.x * blockDim.x + threadIdx.x;
   const int d = blockIdx.y;
-  const int g = blockIdx.z;
+  const int slot = blockIdx.z;
   if (row >= rows)
     return;
-  vt[static_cast<size_t>(g * 128 + d) * ldvt + VtColumn(row)] =
-      qkv[static_cast<size_t>(row) * ld_qkv + (heads + kv_heads + g) * 128 + d];
+  const half_t x = qkv[static_cast<size_t>(row) * ld_qkv + slot * 128 + d];
+  if (slot < heads + kv_heads)
+    qk[static_cast<size_t>(slot) * ldq + static_cast<size_t>(row) * 128 + d] = x;
+  else
+    vt[VtIndex(slot - heads - kv_heads, d, row, ldvt)] = x;
 }
 
 __global__ void RopeRowsKernel(const float2* table, const int* positions,
@@ -375,13 +380,17 @@ void LaunchAddNorm(const AddNormParams& p, hipStream_t stream) {
   Check(hipGetLastError(), "addnorm launch");
 }
 
-void LaunchTransposeV(const half_t* qkv, int ld_qkv, half_t* vt, int ldvt,
-                      int rows, int heads, int kv_heads, hipStream_t stream) {
-  Require(rows > 0 && ldvt >= rows, "transpose: bad rows");
-  const dim3 grid((rows + 255) / 256, 128, kv_heads);
-  Dispatch(TransposeVKernel, grid, dim3(256), 0, stream, true, true, qkv,
-           ld_qkv, vt, ldvt, rows, heads, kv_heads);
-  Check(hipGetLastError(), "transpose launch");
+void LaunchAttentionLayout(const half_t* qkv, int ld_qkv, half_t* qk, int ldq,
+                           half_t* vt, int ldvt, int rows, int heads, int kv_heads,
+                           hipStream_t stream) {
+  Require(rows > 0 && ldvt >= rows && ldvt % 16 == 0 &&
+              static_cast<int64_t>(ldq) >= static_cast<int64_t>(rows) * 128,
+          "attention layout: bad rows");
+  Require(ld_qkv >= (heads + 2 * kv_heads) * 128, "attention layout: rows too narrow");
+  const dim3 grid((rows + 255) / 256, 128, heads + 2 * kv_heads);
+  Dispatch(AttentionLayoutKernel, grid, dim3(256), 0, stream, true, true, qkv,
+           ld_qkv, qk, ldq, vt, ldvt, rows, heads, kv_heads);
+  Check(hipGetLastError(), "attention layout launch");
 }
 
 void LaunchRopeRows(const float2* table, const int* positions, int rows,

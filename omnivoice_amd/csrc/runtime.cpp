@@ -68,6 +68,8 @@ struct Layout {
   std::vector<int> positions;  // [rows_alloc]
   std::vector<int> gather;     // [targets]
   std::vector<AttentionWork> work;
+  int exact_work = 0;    // work[0, exact_work): the exact attention kernel
+  int exact_rounds = 0;  // their largest number of key rounds
   std::vector<ScoreItem> score_items;
   std::vector<SelectItem> select_items;
   std::string signature;
@@ -524,6 +526,7 @@ Layout Engine::Plan(const std::vector<Input>& inputs) const {
                    std::to_string(in.audio_start) + "/" +
                    std::to_string(in.frames);
   }
+  PlanAttentionWork(L.work, &L.exact_work, &L.exact_rounds);
   return L;
 }
 
@@ -531,11 +534,13 @@ void Engine::Prepare(const Layout& L) {
   const std::size_t C = static_cast<std::size_t>(cfg_.audio_codebooks);
   const std::size_t ra = static_cast<std::size_t>(L.rows_alloc);
   const std::size_t h = static_cast<std::size_t>(cfg_.hidden_size);
-  const std::size_t qk_width =
-      static_cast<std::size_t>(cfg_.heads + cfg_.kv_heads) * 128;
+  const std::size_t qk_heads = static_cast<std::size_t>(cfg_.heads + cfg_.kv_heads);
   const std::size_t width =
       static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
   const int ldvt = (L.rows_alloc + 15) / 16 * 16;
+  // q and k head-major: ldvt rows of 128 per head, so that a 32-row tile of
+  // one head is 8 KB of consecutive bytes.
+  const std::size_t ldq = static_cast<std::size_t>(ldvt) * 128;
   Grow(ids_, C * ra);
   Grow(row_kind_, ra);
   Grow(positions_, ra);
@@ -547,7 +552,7 @@ void Engine::Prepare(const Layout& L) {
   Grow(select_items_, L.select_items.size());
   Grow(hidden_, ra * h);
   Grow(normed_, ra * h);
-  Grow(qk_, ra * qk_width);
+  Grow(qk_, qk_heads * ldq);
   Grow(vt_, static_cast<std::size_t>(cfg_.kv_heads) * 128 * ldvt);
   Grow(attn_, ra * static_cast<std::size_t>(cfg_.heads) * 128);
   Grow(act_, ra * static_cast<std::size_t>(cfg_.intermediate_size));
@@ -564,20 +569,23 @@ void Engine::Prepare(const Layout& L) {
       PlanPacked(M, K, static_cast<int>(cfg_.intermediate_size), Epilogue::kPartial).splits);
   Grow(part_, static_cast<std::size_t>(slices) * ra * h);
   // The last key tile of the last sequence reads up to 32 rows past the
-  // packed rows, which no kernel writes: keep those K rows and V^T columns
+  // packed rows, which no kernel writes: keep those K rows and V^T rows
   // zero, since a masked key's probability 0 times a non-finite stale value
   // would still be NaN. (Rows inside the packed range, alignment padding
-  // included, are written by the q/k/v GEMM every layer.) VtColumn permutes
-  // rows inside 16-row blocks, so the V^T clear starts at the block that
-  // holds the last packed row; the GEMM rewrites that block's own rows.
+  // included, are written by the q/k/v GEMM every layer.) V^T is stored in
+  // 16-row blocks (VtIndex), so its clear starts at the block that holds the
+  // last packed row (the GEMM rewrites that block's own rows) and is one
+  // run of whole blocks per kv head.
   const int vt_clear = L.rows & ~15;
-  Check(hipMemsetAsync(qk_.get() + static_cast<std::size_t>(L.rows) * qk_width, 0,
-                       static_cast<std::size_t>(L.rows_alloc - L.rows) * qk_width * sizeof(half_t),
-                       stream_),
+  Check(hipMemset2DAsync(qk_.get() + cfg_.heads * ldq + static_cast<std::size_t>(L.rows) * 128,
+                         ldq * sizeof(half_t), 0,
+                         static_cast<std::size_t>(ldvt - L.rows) * 128 * sizeof(half_t),
+                         static_cast<std::size_t>(cfg_.kv_heads), stream_),
         "clear key slack");
-  Check(hipMemset2DAsync(vt_.get() + vt_clear, static_cast<std::size_t>(ldvt) * sizeof(half_t), 0,
-                         static_cast<std::size_t>(ldvt - vt_clear) * sizeof(half_t),
-                         static_cast<std::size_t>(cfg_.kv_heads) * 128, stream_),
+  Check(hipMemset2DAsync(vt_.get() + VtIndex(0, 0, vt_clear, ldvt),
+                         static_cast<std::size_t>(ldvt) * 128 * sizeof(half_t), 0,
+                         static_cast<std::size_t>(ldvt - vt_clear) * 128 * sizeof(half_t),
+                         static_cast<std::size_t>(cfg_.kv_heads), stream_),
         "clear value slack");
   auto up = [&](void* dst, const void* src, std::size_t bytes) {
     Check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_),
@@ -610,6 +618,7 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
   const int qkv_n = qk_width + static_cast<int>(cfg_.kv_heads) * 128;
   const int heads_width = static_cast<int>(cfg_.heads) * 128;
   const int ldvt = (L.rows_alloc + 15) / 16 * 16;
+  const int ldq = ldvt * 128;  // q/k head stride (head-major)
   const double R = L.real_rows;
   const int C = static_cast<int>(cfg_.audio_codebooks);
   const int Vw = static_cast<int>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
@@ -657,7 +666,9 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
   ap.out = attn_.get();
   ap.work = work_.get();
   ap.work_count = static_cast<int>(L.work.size());
-  ap.ld_qk = qk_width;
+  ap.exact_count = L.exact_work;
+  ap.exact_rounds = L.exact_rounds;
+  ap.ld_qk = ldq;
   ap.ldvt = ldvt;
   ap.heads = static_cast<int>(cfg_.heads);
   ap.kv_heads = static_cast<int>(cfg_.kv_heads);
@@ -696,7 +707,7 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     gemm("gemm_qkv_rope", Epilogue::kQkvRope, normed_.get(), H, W.qkv.get(),
          M, qkv_n, H, R, R * qkv_n * 2.0, [&](GemmParams& p) {
            p.qk = qk_.get();
-           p.ldq = qk_width;
+           p.ldq = ldq;
            p.vt = vt_.get();
            p.ldvt = ldvt;
            p.q_norm = W.q_norm.get();

@@ -31,13 +31,14 @@
 // block stored in the order 0-3, 8-11, 4-7, 12-15 (VtColumn), which makes
 // those eight keys one 16-byte run.
 //
-// A V^T tile is two 16-key blocks of [128 dims][16 keys] (VtIndex), 8 KB of
-// consecutive bytes in memory, copied verbatim into LDS; a lane's 16-byte
-// operand is half of one dim's row of a block, and the 64 lanes of one read
-// cover 1 KB of consecutive LDS. K rows are XOR-swizzled in 16-byte chunks
-// (chunk ^ (key & 15)), so both operand reads are conflict-free.
+// The q/k/v GEMM stores queries, keys and V^T in matrix-core operand order
+// (QkIndex, VtIndex): every 32-row tile of a head is 8 KB of consecutive
+// bytes whose 1 KB blocks are the operands of one MFMA, in lane order. This
+// kernel copies tiles verbatim into LDS; eight lanes of an operand read
+// cover 128 consecutive bytes, so no read has bank conflicts.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "kernels.hpp"
@@ -166,15 +167,9 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
       p.qk + static_cast<size_t>(p.heads + g) * p.ld_qk);
   const unsigned char* v_base = reinterpret_cast<const unsigned char*>(
       p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt);
-  // Lane offsets: K row 4 sub + lane / 16 at swizzled chunk; V^T bytes
-  // 16 lane of the tile's 1 KB block sub.
-  uint32_t k_lane[8];
-#pragma unroll
-  for (int sub = 0; sub < 8; ++sub) {
-    const int key = 4 * sub + (lane >> 4);
-    const int chunk = (lane & 15) ^ (key & 15);
-    k_lane[sub] = static_cast<uint32_t>((lane >> 4) * kHeadDim + 8 * chunk) * 2;
-  }
+  // A K, V^T or query tile is 8 KB of consecutive bytes already in operand
+  // order (QkIndex, VtIndex), copied verbatim: lane l's 16 bytes of 1 KB
+  // block sub at 1024 sub + 16 l.
   const uint32_t v_lane = static_cast<uint32_t>(lane) * 16;
   const uint32_t lds_base = LdsAddress(lds);
   // The r-th round processed is key round (r + shift) % rounds: the query
@@ -199,12 +194,9 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
       const int key0 = work.seq_begin + t * kKTile;
       const uint32_t dst = lds_base + ((r & 1) * kRound + slot_in_round) * kTileBytes +
                            part * 8192 + sub * 1024;
-      if (part == 0) {
-        DmaToLds(k_base + static_cast<size_t>(key0 + 4 * sub) * kHeadDim * 2,
-                 k_lane[sub], dst);
-      } else {
-        DmaToLds(v_base + static_cast<size_t>(key0 >> 4) * 4096 + sub * 1024, v_lane, dst);
-      }
+      DmaToLds((part == 0 ? k_base : v_base) + static_cast<size_t>(key0 >> 4) * 4096 +
+                   sub * 1024,
+               v_lane, dst);
     }
   };
 
@@ -227,19 +219,17 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     return;
   }
   // The group's query tiles (laid out like a K tile; query rows past the
-  // tile's count repeat its last row, whose results are never stored), then
-  // rounds 0 and 1.
+  // tile's count are the rows that follow, whose results are never stored),
+  // then rounds 0 and 1.
 #pragma unroll
   for (int j = 0; j < kQShare; ++j) {
     const int i = wave * kQShare + j;
     const int h = i >> 3, sub = i & 7;
-    const int row = min(4 * sub + (lane >> 4), work.q_count - 1);
-    const int chunk = (lane & 15) ^ ((4 * sub + (lane >> 4)) & 15);
     DmaToLds(reinterpret_cast<const unsigned char*>(
                  p.qk + static_cast<size_t>(g * GROUP + h) * p.ld_qk +
-                 static_cast<size_t>(work.q_begin) * kHeadDim),
-             static_cast<uint32_t>(row * kHeadDim + 8 * chunk) * 2,
-             lds_base + kRingBytes + h * kQBytes + sub * 1024);
+                 static_cast<size_t>(work.q_begin >> 4) * 2048) +
+                 sub * 1024,
+             v_lane, lds_base + kRingBytes + h * kQBytes + sub * 1024);
   }
   issue(0, wave * kShare, Share{});
   if (rounds > 1) {
@@ -255,17 +245,20 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
   for (int dt = 0; dt < 4; ++dt)
     st.o[dt] = floatx16{};
 
-  // Stage-invariant LDS read offsets.
+  // Stage-invariant LDS read offsets: K step kk of a key or query tile
+  // (QkIndex order), and the value-product operand (dims 32 dt .., keys of
+  // block j2; VtIndex order). Eight lanes read 128 consecutive bytes, so
+  // neither read has bank conflicts.
   int k_read[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
-    k_read[kk] = col * 256 + (((2 * kk + half_id) ^ (col & 15)) * 16);
+    k_read[kk] = (col >> 4) * 4096 + kk * 512 + half_id * 256 + (col & 15) * 16;
   int v_read[4][2];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int j2 = 0; j2 < 2; ++j2)
-      v_read[dt][j2] = 8192 + j2 * 4096 + (32 * dt + col) * 32 + half_id * 16;
+      v_read[dt][j2] = 8192 + j2 * 4096 + dt * 1024 + lane * 16;
 
   // Barrier r: round r has landed (every wave waited for its share) and
   // every wave is done with round r - 1, whose ring half then takes round
@@ -399,351 +392,285 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // rescaled while keys stream, and the key quarters' partial outputs merge
 // as a plain sum.
 //
-// One work-group per (32-query tile, kv head): 4 x GROUP compute waves,
-// wave (head h, quarter q) taking key tiles q, q + 4, q + 8, ..., and one
-// producer wave. A key round is four K tiles (one per quarter), a value
-// round the four matching V^T tiles: R = ceil(tiles / 4) key rounds, then
-// R value rounds, through one ring of four rounds (4 x 4 x 8 KB). Only
-// tiles inside the sequence are fetched. The compute waves fetch the
-// queries and the first four rounds, an equal share each (a share is one
-// tile's 1 KB blocks); the producer fetches every later round, round j + 3
-// right after barrier j, which is where every wave has finished round
-// j - 1 in that ring quarter. Compute waves then never wait on a full
-// memory queue between rounds; the producer's issue is paced by its wait
-// counter (at most 63 loads in flight).
+// One work-group per (32-query tile, kv head) with four waves, one per
+// SIMD: wave q takes key tiles q, q + 4, q + 8, ... for all GROUP query
+// heads of the kv head, so every K and V^T operand byte is used by exactly
+// one wave and goes from memory straight into registers (QkIndex and
+// VtIndex store each 32-row tile's operands as whole 256-byte runs), with
+// no LDS staging: the LDS holds only the query tiles, the softmax
+// statistics and the final merge. A wave's tiles stream through a ring of
+// operand buffers, one or two tiles ahead: its key tiles, then its value
+// tiles, so the first value tiles load while the softmax runs. Every load
+// is unconditional (a slot past the wave's last tile re-reads a tile of the
+// sequence and is not used), so the compiler's wait counts stay exact.
 //
 // Between the two phases each wave reduces its scores to a per-query
-// maximum and, after the exchange, a sum, through 1 KB of LDS each; the
-// probabilities are then formed in place and kept as the fp16 MFMA
-// operand. Scores of up to MAXR key rounds live in registers (16 floats per
-// lane and round), so MAXR = 6 covers 768 keys (a 32 x 768 score block per
-// head), the most that fits beside the producer wave without spilling.
+// maximum and, after the exchange, a sum, through LDS; the probabilities
+// are then formed in place and kept as the fp16 MFMA operand. Scores of up
+// to MAXR tiles per wave live in registers (16 floats per lane, tile and
+// head), so MAXR = 6 covers 768 keys.
 constexpr int kExactKeys = 768;
-constexpr int kExactRing = 4;                 // rounds held by the ring
-constexpr int kSlot = 8192;                   // one 32-key K or V^T tile
-constexpr int kRoundBytes = kRound * kSlot;   // one round: four tiles
-constexpr int kExactRingBytes = kExactRing * kRoundBytes;
+constexpr int kExactMaxTiles = 6;   // per wave: 4 x 6 x 32 = 768 keys
+
+// Calls f(integral_constant<int, J>) for J = 0, 1, ...: a loop whose index
+// is a compile-time constant in every iteration.
+template <typename F, int... J>
+__device__ __forceinline__ void UnrollEach(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
 
 template <int GROUP>
 constexpr int ExactLds() {
-  const int ring = kExactRingBytes + GROUP * kQBytes + 2 * GROUP * kRound * 32 * 4;
-  const int merge = 4 * GROUP * 3 * 4 * 64 * 16;  // three O^T slices per wave
-  return ring > merge ? ring : merge;
+  const int front = GROUP * kQBytes + 2 * GROUP * kRound * 32 * 4;  // queries, statistics
+  const int merge = 4 * 3 * GROUP * 16 * 64 * 4;                    // three O^T slices per head
+  return front > merge ? front : merge;
 }
 
 template <int GROUP, int MAXR>
-__global__ __launch_bounds__((4 * GROUP + 1) * 64) void ExactAttentionKernel(AttentionParams p) {
+__global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
     PrefetchRanges(p, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
     return;
   }
-  constexpr int kWaves = 4 * GROUP;           // compute waves; wave kWaves: producer
-  constexpr int kPieces = 32 / kWaves;        // a compute wave's 1 KB DMAs per early round
-  constexpr int kQPieces = 8 * GROUP / kWaves;
-  static_assert(kPieces == 4 || kPieces == 8, "a wave's share is half or all of one tile");
   extern __shared__ __align__(16) unsigned char lds[];
   const int g = blockIdx.x % p.kv_heads;
   const AttentionWork work = p.work[blockIdx.x / p.kv_heads];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tiles = (work.seq_length + kKTile - 1) / kKTile;
-  const int rounds = (tiles + kRound - 1) / kRound;
-  const int total = 2 * rounds;
-  const int early = min(kExactRing, total);   // rounds the compute waves fetch
-
-  const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
-      p.qk + static_cast<size_t>(p.heads + g) * p.ld_qk);
-  const unsigned char* v_base = reinterpret_cast<const unsigned char*>(
-      p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt);
-  // K block `sub` (keys 4 sub .. + 3): lane's key 4 sub + lane / 16 at its
-  // swizzled chunk; the offset depends on sub % 4 only.
-  uint32_t k_lane[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = 4 * i + (lane >> 4);
-    k_lane[i] = static_cast<uint32_t>((lane >> 4) * kHeadDim + 8 * ((lane & 15) ^ key)) * 2;
-  }
-  const uint32_t lds_base = LdsAddress(lds);
-  // Tiles of round j inside the sequence (round j: key round j, or value
-  // round j - rounds).
-  auto round_tiles = [&](int j) {
-    const int r = j < rounds ? j : j - rounds;
-    return min(kRound, tiles - kRound * r);
-  };
-  // 1 KB block `sub` of tile s of round j: keys 4 sub .. 4 sub + 3 of a K
-  // tile, or bytes 1024 sub .. of a V^T tile (8 KB of consecutive bytes).
-  auto dma = [&](int j, int s, int sub, uint32_t k_offset) {
-    const bool keys = j < rounds;
-    const int t = kRound * (keys ? j : j - rounds) + s;
-    const int key0 = work.seq_begin + t * kKTile;
-    const uint32_t dst = lds_base + (j % kExactRing) * kRoundBytes + s * kSlot + sub * 1024;
-    if (keys)
-      DmaToLds(k_base + static_cast<size_t>(key0 + 4 * sub) * kHeadDim * 2, k_offset, dst);
-    else
-      DmaToLds(v_base + static_cast<size_t>(key0 >> 4) * 4096 + sub * 1024,
-               static_cast<uint32_t>(lane) * 16, dst);
-  };
-
-  if (wave == kWaves) {
-    // The producer: rounds early .. total - 1, round j + 3 after barrier j;
-    // before barrier j it waits for its blocks of round j (rounds up to
-    // j + 2 are in flight then). Its barriers pair one to one with the
-    // compute waves': one per round, two for the softmax exchanges after
-    // the last key round, two for the merge.
-    for (int j = 0; j < total; ++j) {
-      if (j >= early) {
-        int later = 0;
-        for (int i = j + 1; i <= min(j + 2, total - 1); ++i)
-          later += round_tiles(i);
-        switch (later) {
-          case 0: WaitLoads<0>(); break;
-          case 1: WaitLoads<8>(); break;
-          case 2: WaitLoads<16>(); break;
-          case 3: WaitLoads<24>(); break;
-          case 4: WaitLoads<32>(); break;
-          case 5: WaitLoads<40>(); break;
-          case 6: WaitLoads<48>(); break;
-          case 7: WaitLoads<56>(); break;
-          default: WaitLoads<63>(); break;
-        }
-      }
-      RingBarrier();
-      const int next = j + kExactRing - 1;
-      if (j >= 1 && next < total) {
-        const int count = round_tiles(next);
-        for (int s = 0; s < count; ++s)
-#pragma unroll
-          for (int sub = 0; sub < 8; ++sub)
-            dma(next, s, sub, k_lane[sub & 3]);
-      }
-      if (j == rounds - 1) {
-        RingBarrier();
-        RingBarrier();
-      }
-    }
-    RingBarrier();
-    RingBarrier();
-    return;
-  }
-
-  const int head_local = wave % GROUP;
-  const int quarter = wave / GROUP;
-  const int head = g * GROUP + head_local;
+  const int lane = threadIdx.x & 63;
+  const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half_id = lane >> 5;
   const int col = lane & 31;
-  // This wave's share of an early round: blocks sub0 .. sub0 + kPieces - 1
-  // (sub0 is 0 or 4) of the round's tile `slot`.
-  const int slot = wave * kPieces / 8;
-  const int sub0 = wave * kPieces % 8;
-  auto fills = [&](int j) { return slot < round_tiles(j); };
+  const int tiles = (work.seq_length + kKTile - 1) / kKTile;
+  const int mine = (tiles - quarter + kRound - 1) / kRound;  // tiles 4 j + quarter < tiles
+  const int block0 = work.seq_begin >> 4;
 
-  // The group's query tiles (rows past the tile's count repeat its last
-  // row, whose results are never stored), then the early rounds.
+  // The group's query tiles into LDS by DMA, verbatim (8 KB of consecutive
+  // bytes per head; rows past the tile's count belong to the next rows and
+  // their results are never stored): GROUP x 8 blocks of 1 KB, 2 GROUP per
+  // wave.
+  const uint32_t lds_base = LdsAddress(lds);
 #pragma unroll
-  for (int i = 0; i < kQPieces; ++i) {
-    const int piece = wave * kQPieces + i;
+  for (int i = 0; i < 2 * GROUP; ++i) {
+    const int piece = quarter * 2 * GROUP + i;
     const int h = piece >> 3, sub = piece & 7;
-    const int row = min(4 * sub + (lane >> 4), work.q_count - 1);
-    const int chunk = (lane & 15) ^ ((4 * sub + (lane >> 4)) & 15);
     DmaToLds(reinterpret_cast<const unsigned char*>(
                  p.qk + static_cast<size_t>(g * GROUP + h) * p.ld_qk +
-                 static_cast<size_t>(work.q_begin) * kHeadDim),
-             static_cast<uint32_t>(row * kHeadDim + 8 * chunk) * 2,
-             lds_base + kExactRingBytes + h * kQBytes + sub * 1024);
+                 static_cast<size_t>(work.q_begin >> 4) * 2048) +
+                 sub * 1024,
+             static_cast<uint32_t>(lane) * 16, lds_base + h * kQBytes + sub * 1024);
   }
-  for (int j = 0; j < early; ++j)
-    if (fills(j))
-#pragma unroll
-      for (int i = 0; i < kPieces; ++i)
-        dma(j, slot, sub0 + i, k_lane[i & 3]);
-  // Barrier j: round j has landed and every wave is done with round j - 1.
-  // A compute wave waits only for its own early blocks.
-  auto begin_round = [&](int j) {
-    if (j < early) {
-      int later = 0;
-      for (int i = j + 1; i < early; ++i)
-        later += fills(i) ? 1 : 0;
-      switch (later) {
-        case 0: WaitLoads<0>(); break;
-        case 1: WaitLoads<kPieces>(); break;
-        case 2: WaitLoads<2 * kPieces>(); break;
-        default: WaitLoads<3 * kPieces>(); break;
-      }
-    }
-    RingBarrier();
-  };
 
-  // LDS read offsets: K (and the query tile, laid out alike) row col,
-  // chunk 2 kk + half_id; V^T dim 32 dt + col of 16-key block j2, the
-  // 16 bytes at 16 half_id.
-  int k_read[8];
+  // Operand offsets (halves) inside a 32-row tile: K step kk of the key
+  // operand; value-product operand f = 2 dt + j2 (dims 32 dt .., keys of
+  // block j2).
+  int k_off[8], v_off[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
-    k_read[kk] = col * 256 + (((2 * kk + half_id) ^ (col & 15)) * 16);
-  int v_read[4][2];
+    k_off[kk] = (col >> 4) * 2048 + kk * 256 + half_id * 128 + (col & 15) * 8;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int f = 0; f < 8; ++f)
+    v_off[f] = (f & 1) * 2048 + (f >> 1) * 512 + lane * 8;
+  const half_t* k_head = p.qk + static_cast<size_t>(p.heads + g) * p.ld_qk;
+  const half_t* v_head = p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt;
+  // Stream slot s: key tile s (s < MAXR), else value tile s - MAXR, of this
+  // wave; slots past its last tile re-read the sequence's last tile. A ring
+  // of kDepth operand buffers, loads kDepth - 1 slots ahead (two buffers at
+  // six tiles, where a third would not fit in registers).
+  constexpr int kDepth = MAXR >= 6 ? 2 : 3;
+  half8 buf[kDepth][8];
+  auto load_slot = [&](auto slot) {
+    constexpr int s = decltype(slot)::value;
+    constexpr int j = s < MAXR ? s : s - MAXR;
+    const int t = min(kRound * j + quarter, tiles - 1);
+    const half_t* base = (s < MAXR ? k_head : v_head) + static_cast<size_t>(block0 + 2 * t) * 2048;
 #pragma unroll
-    for (int j2 = 0; j2 < 2; ++j2)
-      v_read[dt][j2] = j2 * 4096 + (32 * dt + col) * 32 + half_id * 16;
+    for (int f = 0; f < 8; ++f)
+      buf[s % kDepth][f] = *reinterpret_cast<const half8*>(base + (s < MAXR ? k_off[f] : v_off[f]));
+    // Slots issue in stream order: a key tile's operands never queue behind
+    // a later value tile's.
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_slot(std::integral_constant<int, 0>{});
+  if constexpr (kDepth == 3)
+    load_slot(std::integral_constant<int, 1>{});
+  // The query DMAs were issued before the operand loads (8 per slot).
+  WaitLoads<8 * (kDepth - 1)>();
+  RingBarrier();
+  half8 qf[GROUP][8];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      qf[h][kk] = *reinterpret_cast<const half8*>(
+          lds + h * kQBytes + (col >> 4) * 4096 + kk * 512 + half_id * 256 + (col & 15) * 16);
 
-  // Key phase: S^T = K Q^T per tile; lane holds keys 8 (e / 4) + 4 half_id
-  // + e % 4 of its query column, scaled by log2(e) / sqrt(128); keys past
-  // the sequence are -inf. Up to four rounds the query fragments stay in
-  // registers; with six they are re-read from LDS every round (registers).
-  constexpr bool kHoldQ = MAXR <= 4;
-  const unsigned char* qs = lds + kExactRingBytes + head_local * kQBytes;
-  half8 qf[kHoldQ ? 8 : 1];
-  floatx16 s[MAXR];
+  // Key phase: S^T = K Q^T per tile and head, unscaled; lane holds keys
+  // 8 (e / 4) + 4 half_id + e % 4 of its query column. Keys past the
+  // sequence (only in its last, partial tile) are -inf.
+  floatx16 s[GROUP][MAXR];
+  auto key_tile = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (j + kDepth - 1 < 2 * MAXR)
+      load_slot(std::integral_constant<int, j + kDepth - 1>{});
+    if (j < mine) {
+      const int valid_keys = work.seq_length - (kRound * j + quarter) * kKTile;
 #pragma unroll
-  for (int j = 0; j < MAXR; ++j) {
-    if (j < rounds) {
-      begin_round(j);
-      if constexpr (kHoldQ) {
-        if (j == 0)
-#pragma unroll
-          for (int kk = 0; kk < 8; ++kk)
-            qf[kk] = *reinterpret_cast<const half8*>(qs + k_read[kk]);
-      }
-      const int t = kRound * j + quarter;
-      if (t < tiles) {
-        const unsigned char* tile = lds + (j % kExactRing) * kRoundBytes + quarter * kSlot;
+      for (int h = 0; h < GROUP; ++h) {
         floatx16 acc = floatx16{};
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          half8 q;
-          if constexpr (kHoldQ)
-            q = qf[kk];
-          else
-            q = *reinterpret_cast<const half8*>(qs + k_read[kk]);
-          acc = Mfma32(*reinterpret_cast<const half8*>(tile + k_read[kk]), q, acc);
-        }
-        const int valid_keys = work.seq_length - t * kKTile;
+        for (int kk = 0; kk < 8; ++kk)
+          acc = Mfma32(buf[j % kDepth][kk], qf[h][kk], acc);
+        s[h][j] = acc;
+        if (valid_keys < kKTile)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = 8 * (e / 4) + 4 * half_id + (e & 3);
-          s[j][e] = key < valid_keys ? acc[e] * p.scale_log2 : -__builtin_inff();
-        }
+          for (int e = 0; e < 16; ++e) {
+            const int key = 8 * (e / 4) + 4 * half_id + (e & 3);
+            s[h][j][e] = key < valid_keys ? s[h][j][e] : -__builtin_inff();
+          }
       }
     }
-  }
+  };
+  UnrollEach(key_tile, std::make_integer_sequence<int, MAXR>{});
 
   // Exact softmax over all keys: per-query maximum of the four quarters,
-  // then the sum of exp2(s - max), then p = fp16(exp2(s - max) / sum).
-  float* smax = reinterpret_cast<float*>(lds + kExactRingBytes + GROUP * kQBytes);
+  // then the sum of e = exp2(c s - c max), c = log2(e) / sqrt(128) (c > 0,
+  // so the maximum of the unscaled scores serves), then p = fp16(e / sum).
+  float* smax = reinterpret_cast<float*>(lds + GROUP * kQBytes);
   float* ssum = smax + GROUP * kRound * 32;
-  float m = -__builtin_inff();
+  float inverse[GROUP];
+  {
+    float m[GROUP];
 #pragma unroll
-  for (int j = 0; j < MAXR; ++j)
-    if (j < rounds && kRound * j + quarter < tiles)
+    for (int h = 0; h < GROUP; ++h) {
+      m[h] = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        m = fmaxf(m, s[j][e]);
-  m = fmaxf(m, __shfl_xor(m, 32));
-  const int stat = (head_local * kRound + quarter) * 32 + col;
-  if (half_id == 0)
-    smax[stat] = m;
-  RingBarrier();
-  const float* hmax = smax + head_local * kRound * 32 + col;
-  const float row_max = fmaxf(fmaxf(hmax[0], hmax[32]), fmaxf(hmax[64], hmax[96]));
-  float sum = 0.0F;
+      for (int j = 0; j < MAXR; ++j)
+        if (j < mine)
 #pragma unroll
-  for (int j = 0; j < MAXR; ++j)
-    if (j < rounds && kRound * j + quarter < tiles)
+          for (int e = 0; e < 16; ++e)
+            m[h] = fmaxf(m[h], s[h][j][e]);
+      m[h] = fmaxf(m[h], __shfl_xor(m[h], 32));
+      if (half_id == 0)
+        smax[(h * kRound + quarter) * 32 + col] = m[h];
+    }
+    RingBarrier();
+    float sum[GROUP];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[j][e] = __builtin_amdgcn_exp2f(s[j][e] - row_max);
-        sum += s[j][e];
-      }
-  sum += __shfl_xor(sum, 32);
-  if (half_id == 0)
-    ssum[stat] = sum;
-  RingBarrier();
-  const float* hsum = ssum + head_local * kRound * 32 + col;
-  const float inverse = 1.0F / ((hsum[0] + hsum[32]) + (hsum[64] + hsum[96]));
+    for (int h = 0; h < GROUP; ++h) {
+      const float* hm = smax + h * kRound * 32 + col;
+      const float shift = -(fmaxf(fmaxf(hm[0], hm[32]), fmaxf(hm[64], hm[96])) * p.scale_log2);
+      sum[h] = 0.0F;
+#pragma unroll
+      for (int j = 0; j < MAXR; ++j)
+        if (j < mine)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            s[h][j][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][j][e], p.scale_log2, shift));
+            sum[h] += s[h][j][e];
+          }
+      sum[h] += __shfl_xor(sum[h], 32);
+      if (half_id == 0)
+        ssum[(h * kRound + quarter) * 32 + col] = sum[h];
+    }
+    RingBarrier();
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h) {
+      const float* hs = ssum + h * kRound * 32 + col;
+      inverse[h] = 1.0F / ((hs[0] + hs[32]) + (hs[64] + hs[96]));
+    }
+  }
   // P^T operand for keys 16 j2 .. 16 j2 + 15 of a tile: slot e is
-  // accumulator element 8 j2 + e; V^T's permuted block order puts the same
-  // keys in the 16 bytes at position 8 half_id of the block.
-  half8 pf[MAXR][2];
+  // accumulator element 8 j2 + e; VtIndex puts the same keys in the chunk
+  // of lane half half_id.
+  half8 pf[GROUP][MAXR][2];
 #pragma unroll
-  for (int j = 0; j < MAXR; ++j)
-    if (j < rounds && kRound * j + quarter < tiles)
+  for (int h = 0; h < GROUP; ++h)
 #pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          pf[j][j2][e] = static_cast<half_t>(s[j][8 * j2 + e] * inverse);
-
-  // Value phase: O^T = V^T P^T over this quarter's tiles.
-  floatx16 o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-    o[dt] = floatx16{};
-#pragma unroll
-  for (int j = 0; j < MAXR; ++j) {
-    if (j < rounds) {
-      begin_round(rounds + j);
-      if (kRound * j + quarter < tiles) {
-        const unsigned char* tile =
-            lds + ((rounds + j) % kExactRing) * kRoundBytes + quarter * kSlot;
+    for (int j = 0; j < MAXR; ++j)
+      if (j < mine)
 #pragma unroll
         for (int j2 = 0; j2 < 2; ++j2)
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt)
-            o[dt] = Mfma32(*reinterpret_cast<const half8*>(tile + v_read[dt][j2]),
-                           pf[j][j2], o[dt]);
-      }
-    }
-  }
+          for (int e = 0; e < 8; ++e)
+            pf[h][j][j2][e] = static_cast<half_t>(s[h][j][8 * j2 + e] * inverse[h]);
 
-  // The four quarters' outputs are summed as ((0 + 1) + (2 + 3)); wave
-  // (head, quarter) finishes dims 32 quarter .. + 31 of its head, its own
-  // part straight from registers. Every DMA has landed (each wave waited
-  // for its last one before the last round's barrier), so the ring is free
-  // once every wave is past that round.
+  // Value phase: O^T = V^T P^T over this quarter's tiles, every head.
+  floatx16 o[GROUP][4];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      o[h][dt] = floatx16{};
+  auto value_tile = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    constexpr int slot = MAXR + j;
+    if constexpr (slot + kDepth - 1 < 2 * MAXR)
+      load_slot(std::integral_constant<int, slot + kDepth - 1>{});
+    if (j < mine) {
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int h = 0; h < GROUP; ++h)
+            o[h][dt] = Mfma32(buf[slot % kDepth][2 * dt + j2], pf[h][j][j2], o[h][dt]);
+    }
+  };
+  UnrollEach(value_tile, std::make_integer_sequence<int, MAXR>{});
+
+  // The four quarters' outputs are summed as ((0 + 1) + (2 + 3)); wave q
+  // finishes dims 32 q .. + 31 of every head, its own part straight from
+  // registers. The queries and statistics are dead once every wave is past
+  // the barrier, so the merge reuses their space.
   floatx4* accs = reinterpret_cast<floatx4*>(lds);
   RingBarrier();
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    if (dt == quarter)
-      continue;
-    const int part = dt < quarter ? dt : dt - 1;
+  for (int h = 0; h < GROUP; ++h)
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      accs[((wave * 3 + part) * 4 + k) * 64 + lane] =
-          floatx4{o[dt][4 * k], o[dt][4 * k + 1], o[dt][4 * k + 2], o[dt][4 * k + 3]};
-  }
-  RingBarrier();
-  const floatx16 own = quarter == 0 ? o[0] : quarter == 1 ? o[1] : quarter == 2 ? o[2] : o[3];
-  auto load = [&](int q) {
-    if (q == quarter)
-      return own;
-    const int w = q * GROUP + head_local;
-    const int part = quarter < q ? quarter : quarter - 1;
-    floatx16 v;
+    for (int dt = 0; dt < 4; ++dt) {
+      if (dt == quarter)
+        continue;
+      const int part = dt < quarter ? dt : dt - 1;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const floatx4 x = accs[((w * 3 + part) * 4 + k) * 64 + lane];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[4 * k + i] = x[i];
+      for (int k = 0; k < 4; ++k)
+        accs[(((quarter * 3 + part) * GROUP + h) * 4 + k) * 64 + lane] =
+            floatx4{o[h][dt][4 * k], o[h][dt][4 * k + 1], o[h][dt][4 * k + 2],
+                    o[h][dt][4 * k + 3]};
     }
-    return v;
-  };
-  const floatx16 result = (load(0) + load(1)) + (load(2) + load(3));
+  RingBarrier();
   if (col >= work.q_count)
     return;
-  half_t* out = p.out + static_cast<size_t>(work.q_begin + col) * p.heads * kHeadDim +
-                head * kHeadDim + quarter * 32;
-  // Lane holds dims 8 (e / 4) + 4 half_id + e % 4 of the slice.
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    half4 v;
+  for (int h = 0; h < GROUP; ++h) {
+    const floatx16 own = quarter == 0   ? o[h][0]
+                         : quarter == 1 ? o[h][1]
+                         : quarter == 2 ? o[h][2]
+                                        : o[h][3];
+    auto load = [&](int q) {
+      if (q == quarter)
+        return own;
+      const int part = quarter < q ? quarter : quarter - 1;
+      floatx16 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = static_cast<half_t>(result[4 * q + e]);
-    *reinterpret_cast<half4*>(out + 8 * q + 4 * half_id) = v;
+      for (int k = 0; k < 4; ++k) {
+        const floatx4 x = accs[(((q * 3 + part) * GROUP + h) * 4 + k) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[4 * k + i] = x[i];
+      }
+      return v;
+    };
+    const floatx16 result = (load(0) + load(1)) + (load(2) + load(3));
+    half_t* out = p.out + static_cast<size_t>(work.q_begin + col) * p.heads * kHeadDim +
+                  (g * GROUP + h) * kHeadDim + quarter * 32;
+    // Lane holds dims 8 (e / 4) + 4 half_id + e % 4 of the slice.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      half4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = static_cast<half_t>(result[4 * q + e]);
+      *reinterpret_cast<half4*>(out + 8 * q + 4 * half_id) = v;
+    }
   }
 }
 
@@ -780,26 +707,31 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   Require(p.exact_count == 0 ||
               (p.exact_rounds >= 1 && p.exact_rounds * kRound * kKTile <= kExactAttentionKeys),
           "attention: exact key rounds outside 1 .. 6");
-  static_assert(kExactAttentionKeys == kExactKeys, "exact kernel key limit");
+  static_assert(kExactAttentionKeys == kExactKeys &&
+                    kExactKeys == kExactMaxTiles * kRound * kKTile,
+                "exact kernel key limit");
   const bool online = p.exact_count < p.work_count;
   if (p.exact_count > 0) {
     AttentionParams e = p;
     e.work_count = p.exact_count;
     const dim3 grid(e.work_count * e.kv_heads + e.prefetch_groups);
-    const int r = p.exact_rounds;
-    auto launch = [&](auto kernel, int waves, int lds_bytes) {
-      Dispatch(kernel, grid, dim3(waves * 64), lds_bytes, stream, true, !online, e);
+    auto launch = [&](auto kernel, int lds_bytes) {
+      Dispatch(kernel, grid, dim3(256), lds_bytes, stream, true, !online, e);
     };
-    if (group == 1) {
-      if (r <= 1) launch(ExactAttentionKernel<1, 1>, 5, ExactLds<1>());
-      else if (r <= 2) launch(ExactAttentionKernel<1, 2>, 5, ExactLds<1>());
-      else if (r <= 4) launch(ExactAttentionKernel<1, 4>, 5, ExactLds<1>());
-      else launch(ExactAttentionKernel<1, 6>, 5, ExactLds<1>());
-    } else {
-      if (r <= 1) launch(ExactAttentionKernel<2, 1>, 9, ExactLds<2>());
-      else if (r <= 2) launch(ExactAttentionKernel<2, 2>, 9, ExactLds<2>());
-      else if (r <= 4) launch(ExactAttentionKernel<2, 4>, 9, ExactLds<2>());
-      else launch(ExactAttentionKernel<2, 6>, 9, ExactLds<2>());
+    // The kernel instance holds exactly the largest per-wave tile count.
+    switch (group * 8 + p.exact_rounds) {
+      case 9: launch(ExactAttentionKernel<1, 1>, ExactLds<1>()); break;
+      case 10: launch(ExactAttentionKernel<1, 2>, ExactLds<1>()); break;
+      case 11: launch(ExactAttentionKernel<1, 3>, ExactLds<1>()); break;
+      case 12: launch(ExactAttentionKernel<1, 4>, ExactLds<1>()); break;
+      case 13: launch(ExactAttentionKernel<1, 5>, ExactLds<1>()); break;
+      case 14: launch(ExactAttentionKernel<1, 6>, ExactLds<1>()); break;
+      case 17: launch(ExactAttentionKernel<2, 1>, ExactLds<2>()); break;
+      case 18: launch(ExactAttentionKernel<2, 2>, ExactLds<2>()); break;
+      case 19: launch(ExactAttentionKernel<2, 3>, ExactLds<2>()); break;
+      case 20: launch(ExactAttentionKernel<2, 4>, ExactLds<2>()); break;
+      case 21: launch(ExactAttentionKernel<2, 5>, ExactLds<2>()); break;
+      default: launch(ExactAttentionKernel<2, 6>, ExactLds<2>()); break;
     }
   }
   if (online) {

@@ -18,7 +18,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kWave = 64;
 
 // Each packed sequence starts at a multiple of this many rows, so that its
-// 32-key tiles of V^T are two whole 16-row blocks (see VtIndex).
+// 32-row tiles are two whole 16-row blocks of the attention's operand
+// layouts (QkIndex, VtIndex).
 constexpr int kSequenceAlign = 16;
 
 // Column of packed row `row` in V^T: within every 16-row block the rows are
@@ -29,14 +30,30 @@ __host__ __device__ constexpr int VtColumn(int row) {
          (row & 3);
 }
 
-// V^T layout: per kv head, `ldvt` rows (a multiple of 16) in blocks of 16
-// rows; block b is [128 dims][16 rows] fp16 (4 KB), the rows in VtColumn
-// order. A 32-key tile that starts on a 16-row boundary is then 8 KB of
-// consecutive bytes, which the attention fetches as whole cache lines.
-// Element index of (kv head g, dim d, packed row `row`):
+// The attention's operands are stored in matrix-core fragment order, in
+// blocks of 16 packed rows (4 KB per head and block), so that the operand of
+// one v_mfma_f32_32x32x16_f16 for a 32-row tile is whole 256-byte runs that
+// a wave loads straight into registers.
+//
+// q and k heads: head h's rows at h * ldq; block b (rows 16 b .. + 15) is
+// [K step kk 8][half 2][row 16] of 16-byte chunks, chunk (kk, half, r)
+// holding dims 16 kk + 8 half .. + 7 of row 16 b + r. The A (keys) or B
+// (queries) operand of K step kk for the tile at block b is lane l: chunk
+// (kk, l / 32, l % 16) of block b + (l % 32) / 16.
+__host__ __device__ constexpr std::size_t QkIndex(int head, int row, int dim, std::size_t ldq) {
+  return static_cast<std::size_t>(head) * ldq + static_cast<std::size_t>(row >> 4) * 2048 +
+         (dim >> 4) * 256 + ((dim >> 3) & 1) * 128 + (row & 15) * 8 + (dim & 7);
+}
+
+// V^T of kv head g: `ldvt` rows (a multiple of 16) at g * 128 * ldvt; block
+// b is [dim group dt 4][half 2][dim 32] of 16-byte chunks, chunk (dt, half,
+// d) holding dim 32 dt + d of the 8 rows at VtColumn positions 8 half .. + 7
+// of the block. The A operand (32 dims x 16 keys) of the value product for
+// dims 32 dt .. + 31 and the keys of block b is lane l: chunk (dt, l / 32,
+// l % 32) of block b, 1 KB of consecutive bytes.
 __host__ __device__ constexpr std::size_t VtIndex(int g, int d, int row, int ldvt) {
-  return (static_cast<std::size_t>(g) * 128 * ldvt) +
-         static_cast<std::size_t>(row >> 4) * 2048 + d * 16 + (VtColumn(row) & 15);
+  return static_cast<std::size_t>(g) * 128 * ldvt + static_cast<std::size_t>(row >> 4) * 2048 +
+         (d >> 5) * 512 + ((VtColumn(row) >> 3) & 1) * 256 + (d & 31) * 8 + (VtColumn(row) & 7);
 }
 
 // Output stores that write through to memory: relaxed device-scope atomic

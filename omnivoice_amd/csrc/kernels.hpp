@@ -64,8 +64,8 @@ enum class Epilogue : int {
   kStore = 0,       // y fp32 [M][ldc] = acc
   kAccumulate = 1,  // y fp32 [M][ldc] += acc (the residual stream)
   kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
-                    // qk, head-major: element (head, row, d) at
-                    // head * ldq + row * 128 + d; v heads -> fp16 V^T
+                    // qk at QkIndex(head, row, d, ldq); v heads ->
+                    // fp16 V^T at VtIndex
                     // vt[g][d][VtColumn(row)] (ldvt % 16 == 0)
   kSwiGlu = 3,      // act fp16 [M][ldh] = silu(gate) * up; the W rows pair
                     // gate and up rows: per 128-row tile 64 gate rows then
@@ -198,7 +198,7 @@ struct AddNormParams {
 void LaunchAddNorm(const AddNormParams& p, hipStream_t stream);
 
 // The attention's operand layouts from row-major q|k|v rows (r < rows):
-// qk[h * ldq + r * 128 + d] = qkv[r][h * 128 + d] for the q and k heads,
+// qk[QkIndex(h, r, d, ldq)] = qkv[r][h * 128 + d] for the q and k heads,
 // vt[VtIndex(g, d, r, ldvt)] = qkv[r][(heads + kv_heads + g) * 128 + d].
 void LaunchAttentionLayout(const half_t* qkv, int ld_qkv, half_t* qk, int ldq,
                            half_t* vt, int ldvt, int rows, int heads, int kv_heads,
@@ -216,9 +216,8 @@ struct AttentionWork {
   int q_begin, q_count, seq_begin, seq_length;
 };
 struct AttentionParams {
-  const half_t* qk;        // head-major: q heads then k heads, element
-                           // (head, row, d) at head * ld_qk + row * 128 + d
-  const half_t* vt;        // [kv_heads][128][ldvt], columns by VtColumn
+  const half_t* qk;        // q heads then k heads at QkIndex(head, row, d, ld_qk)
+  const half_t* vt;        // V^T at VtIndex(g, d, row, ldvt)
   half_t* out;             // [rows][heads * 128]
   const AttentionWork* work;
   int work_count;

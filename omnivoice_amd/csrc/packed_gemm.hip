@@ -302,31 +302,31 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           const int m = m0 + 32 * b + col;
           if (m >= p.m)
             continue;
-          half_t* column = p.vt + VtIndex(gv, 0, m, p.ldvt);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
-            column[d * 16] = static_cast<half_t>(acc[wb][b][r]);
+            p.vt[VtIndex(gv, d, m, p.ldvt)] = static_cast<half_t>(acc[wb][b][r]);
           }
         }
       }
     }
     Barrier();
     if (qk) {
-      // The 4 / WB waves of this head copy its staged rows out, 16 lanes per
-      // 256-byte row.
-      constexpr int kGroup = 4 / WB;
-      constexpr int kRowsPerPass = 4 * kGroup;
-      const int t = (wave % kGroup) * 64 + lane;
-      const int q = t & 15;
+      // The 4 / WB waves of this head copy its staged rows out in the
+      // attention's fragment order (QkIndex): 16 lanes store chunk q of 16
+      // consecutive rows, one 256-byte run.
+      constexpr int kLanes = 64 * (4 / WB);
+      const int t = (wave % (4 / WB)) * 64 + lane;
 #pragma unroll
-      for (int pass = 0; pass < 32 * XB / kRowsPerPass; ++pass) {
-        const int r = pass * kRowsPerPass + (t >> 4);
+      for (int pass = 0; pass < 32 * XB * 16 / kLanes; ++pass) {
+        const int e = pass * kLanes + t;
+        const int r = (e & 15) + 16 * (e >> 8);
+        const int q = (e >> 4) & 15;
         const int m = m0 + r;
         const half8 v =
             *reinterpret_cast<const half8*>(lds + stage + r * 256 + ((q ^ (r & 15)) << 4));
         if (m < p.m)
-          *reinterpret_cast<half8*>(p.qk + static_cast<size_t>(slot) * p.ldq + m * 128 + 8 * q) = v;
+          *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m, 8 * q, p.ldq)) = v;
       }
     }
   }

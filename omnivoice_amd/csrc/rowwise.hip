@@ -295,7 +295,7 @@ __global__ __launch_bounds__(64) void AddNorm1024Kernel(AddNormParams p) {
 }
 
 // One thread per (head slot, dim, row): slots below heads + kv_heads are q
-// and k heads (head-major copy), the rest value heads (V^T blocks).
+// and k heads (QkIndex), the rest value heads (VtIndex).
 __global__ void AttentionLayoutKernel(const half_t* qkv, int ld_qkv, half_t* qk, int ldq,
                                       half_t* vt, int ldvt, int rows, int heads,
                                       int kv_heads) {
@@ -306,7 +306,7 @@ __global__ void AttentionLayoutKernel(const half_t* qkv, int ld_qkv, half_t* qk,
     return;
   const half_t x = qkv[static_cast<size_t>(row) * ld_qkv + slot * 128 + d];
   if (slot < heads + kv_heads)
-    qk[static_cast<size_t>(slot) * ldq + static_cast<size_t>(row) * 128 + d] = x;
+    qk[QkIndex(slot, row, d, ldq)] = x;
   else
     vt[VtIndex(slot - heads - kv_heads, d, row, ldvt)] = x;
 }

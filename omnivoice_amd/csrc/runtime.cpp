@@ -538,8 +538,9 @@ void Engine::Prepare(const Layout& L) {
   const std::size_t width =
       static_cast<std::size_t>(cfg_.audio_codebooks * cfg_.audio_vocab_size);
   const int ldvt = (L.rows_alloc + 15) / 16 * 16;
-  // q and k head-major: ldvt rows of 128 per head, so that a 32-row tile of
-  // one head is 8 KB of consecutive bytes.
+  // q and k: ldvt rows per head in the attention's fragment order
+  // (QkIndex), so that a 32-row tile of one head is 8 KB of consecutive
+  // bytes.
   const std::size_t ldq = static_cast<std::size_t>(ldvt) * 128;
   Grow(ids_, C * ra);
   Grow(row_kind_, ra);
@@ -568,23 +569,23 @@ void Engine::Prepare(const Layout& L) {
       PlanPacked(M, K, static_cast<int>(cfg_.heads * 128), Epilogue::kPartial).splits,
       PlanPacked(M, K, static_cast<int>(cfg_.intermediate_size), Epilogue::kPartial).splits);
   Grow(part_, static_cast<std::size_t>(slices) * ra * h);
-  // The last key tile of the last sequence reads up to 32 rows past the
-  // packed rows, which no kernel writes: keep those K rows and V^T rows
+  // The last 32-row tile of the last sequence reads up to 32 rows past the
+  // packed rows, which no kernel writes: keep those q/k rows and V^T rows
   // zero, since a masked key's probability 0 times a non-finite stale value
-  // would still be NaN. (Rows inside the packed range, alignment padding
-  // included, are written by the q/k/v GEMM every layer.) V^T is stored in
-  // 16-row blocks (VtIndex), so its clear starts at the block that holds the
-  // last packed row (the GEMM rewrites that block's own rows) and is one
-  // run of whole blocks per kv head.
-  const int vt_clear = L.rows & ~15;
-  Check(hipMemset2DAsync(qk_.get() + cfg_.heads * ldq + static_cast<std::size_t>(L.rows) * 128,
-                         ldq * sizeof(half_t), 0,
-                         static_cast<std::size_t>(ldvt - L.rows) * 128 * sizeof(half_t),
-                         static_cast<std::size_t>(cfg_.kv_heads), stream_),
-        "clear key slack");
-  Check(hipMemset2DAsync(vt_.get() + VtIndex(0, 0, vt_clear, ldvt),
+  // would still be NaN (and a query row past the sequence, whose results are
+  // dropped, stays finite). Rows inside the packed range, alignment padding
+  // included, are written by the q/k/v GEMM every layer. Both layouts store
+  // rows interleaved in 16-row blocks (QkIndex, VtIndex), so the clear
+  // starts at the block that holds the last packed row (the GEMM rewrites
+  // that block's own rows) and is one run of whole blocks per head.
+  const int slack = L.rows & ~15;
+  Check(hipMemset2DAsync(qk_.get() + QkIndex(0, slack, 0, ldq), ldq * sizeof(half_t), 0,
+                         static_cast<std::size_t>(ldvt - slack) * 128 * sizeof(half_t),
+                         qk_heads, stream_),
+        "clear q/k slack");
+  Check(hipMemset2DAsync(vt_.get() + VtIndex(0, 0, slack, ldvt),
                          static_cast<std::size_t>(ldvt) * 128 * sizeof(half_t), 0,
-                         static_cast<std::size_t>(ldvt - vt_clear) * 128 * sizeof(half_t),
+                         static_cast<std::size_t>(ldvt - slack) * 128 * sizeof(half_t),
                          static_cast<std::size_t>(cfg_.kv_heads), stream_),
         "clear value slack");
   auto up = [&](void* dst, const void* src, std::size_t bytes) {
@@ -732,11 +733,13 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
                                    : nullptr;
         ap.prefetch_bytes[r] = ranges[r] ? ranges[r]->bytes() : 0;
       }
-      // Only where at least a quarter of the CUs would idle: with fewer
-      // prefetch work-groups the reads outlast the attention and delay
-      // everything after it (clone and chunk shapes, measured).
+      // Only where most CUs would idle (the 2 s shape: 40 attention
+      // work-groups): with fewer prefetch work-groups the 31.5 MB outlast
+      // the attention and delay everything after it (10 s shape, 152
+      // work-groups: 535 vs 544 unmask steps/s with and without; clone and
+      // chunk shapes likewise, measured).
       const int busy = ap.work_count * ap.kv_heads;
-      ap.prefetch_groups = busy <= 192 ? 256 - busy : 0;
+      ap.prefetch_groups = busy <= 96 ? 256 - busy : 0;
     }
     Run(prof, "attention", attention_flops, R * (qkv_n + heads_width) * 2.0,
         [&] { LaunchAttention(ap, stream_); });

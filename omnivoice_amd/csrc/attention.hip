@@ -396,9 +396,9 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // SIMD: wave q takes key tiles q, q + 4, q + 8, ... for all GROUP query
 // heads of the kv head, so every K and V^T operand byte is used by exactly
 // one wave and goes from memory straight into registers (QkIndex and
-// VtIndex store each 32-row tile's operands as whole 256-byte runs), with
-// no LDS staging: the LDS holds only the query tiles, the softmax
-// statistics and the final merge. A wave's tiles stream through a ring of
+// VtIndex store each 32-row tile's operands as whole 256-byte runs), as do
+// the query operands (read by all four waves, from L2): the LDS holds only
+// the softmax statistics and the final merge. A wave's tiles stream through a ring of
 // operand buffers, one or two tiles ahead: its key tiles, then its value
 // tiles, so the first value tiles load while the softmax runs. Every load
 // is unconditional (a slot past the wave's last tile re-reads a tile of the
@@ -421,9 +421,9 @@ __device__ __forceinline__ void UnrollEach(F&& f, std::integer_sequence<int, J..
 
 template <int GROUP>
 constexpr int ExactLds() {
-  const int front = GROUP * kQBytes + 2 * GROUP * kRound * 32 * 4;  // queries, statistics
-  const int merge = 4 * 3 * GROUP * 16 * 64 * 4;                    // three O^T slices per head
-  return front > merge ? front : merge;
+  const int stats = 2 * GROUP * kRound * 32 * 4;  // maxima, then sums
+  const int merge = 4 * 3 * GROUP * 16 * 64 * 4;  // three O^T slices per head
+  return stats > merge ? stats : merge;
 }
 
 template <int GROUP, int MAXR>
@@ -442,22 +442,6 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   const int tiles = (work.seq_length + kKTile - 1) / kKTile;
   const int mine = (tiles - quarter + kRound - 1) / kRound;  // tiles 4 j + quarter < tiles
   const int block0 = work.seq_begin >> 4;
-
-  // The group's query tiles into LDS by DMA, verbatim (8 KB of consecutive
-  // bytes per head; rows past the tile's count belong to the next rows and
-  // their results are never stored): GROUP x 8 blocks of 1 KB, 2 GROUP per
-  // wave.
-  const uint32_t lds_base = LdsAddress(lds);
-#pragma unroll
-  for (int i = 0; i < 2 * GROUP; ++i) {
-    const int piece = quarter * 2 * GROUP + i;
-    const int h = piece >> 3, sub = piece & 7;
-    DmaToLds(reinterpret_cast<const unsigned char*>(
-                 p.qk + static_cast<size_t>(g * GROUP + h) * p.ld_qk +
-                 static_cast<size_t>(work.q_begin >> 4) * 2048) +
-                 sub * 1024,
-             static_cast<uint32_t>(lane) * 16, lds_base + h * kQBytes + sub * 1024);
-  }
 
   // Operand offsets (halves) inside a 32-row tile: K step kk of the key
   // operand; value-product operand f = 2 dt + j2 (dims 32 dt .., keys of
@@ -489,19 +473,22 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
     // a later value tile's.
     __builtin_amdgcn_sched_barrier(0);
   };
+  // The query tiles' operands straight into registers (rows past the
+  // tile's count belong to the next rows; their results are never stored),
+  // then the first operand slots.
+  half8 qf[GROUP][8];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) {
+    const half_t* q_tile = p.qk + static_cast<size_t>(g * GROUP + h) * p.ld_qk +
+                           static_cast<size_t>(work.q_begin >> 4) * 2048;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      qf[h][kk] = *reinterpret_cast<const half8*>(q_tile + k_off[kk]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   load_slot(std::integral_constant<int, 0>{});
   if constexpr (kDepth == 3)
     load_slot(std::integral_constant<int, 1>{});
-  // The query DMAs were issued before the operand loads (8 per slot).
-  WaitLoads<8 * (kDepth - 1)>();
-  RingBarrier();
-  half8 qf[GROUP][8];
-#pragma unroll
-  for (int h = 0; h < GROUP; ++h)
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qf[h][kk] = *reinterpret_cast<const half8*>(
-          lds + h * kQBytes + (col >> 4) * 4096 + kk * 512 + half_id * 256 + (col & 15) * 16);
 
   // Key phase: S^T = K Q^T per tile and head, unscaled; lane holds keys
   // 8 (e / 4) + 4 half_id + e % 4 of its query column. Keys past the
@@ -534,7 +521,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   // Exact softmax over all keys: per-query maximum of the four quarters,
   // then the sum of e = exp2(c s - c max), c = log2(e) / sqrt(128) (c > 0,
   // so the maximum of the unscaled scores serves), then p = fp16(e / sum).
-  float* smax = reinterpret_cast<float*>(lds + GROUP * kQBytes);
+  float* smax = reinterpret_cast<float*>(lds);
   float* ssum = smax + GROUP * kRound * 32;
   float inverse[GROUP];
   {
@@ -619,8 +606,8 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
 
   // The four quarters' outputs are summed as ((0 + 1) + (2 + 3)); wave q
   // finishes dims 32 q .. + 31 of every head, its own part straight from
-  // registers. The queries and statistics are dead once every wave is past
-  // the barrier, so the merge reuses their space.
+  // registers. The statistics are dead once every wave is past the
+  // barrier, so the merge reuses their space.
   floatx4* accs = reinterpret_cast<floatx4*>(lds);
   RingBarrier();
 #pragma unroll

@@ -101,40 +101,11 @@ __device__ __forceinline__ Slice Merge(const Slice& a, const Slice& b) {
   return c;
 }
 
-// The prefetch work-groups: each thread keeps eight 16-byte loads in
-// flight (clamped in bounds, no load under a condition) and folds them into
-// a value that is never stored, so only the cache fill remains.
-__device__ __forceinline__ void PrefetchRanges(const AttentionParams& p, int group) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  constexpr int kInFlight = 8;
-  const unsigned long long stride = static_cast<unsigned long long>(p.prefetch_groups) * blockDim.x;
-  unsigned int fold = 0;
-  for (int r = 0; r < AttentionParams::kMaxPrefetch; ++r) {
-    const unsigned long long chunks = p.prefetch_bytes[r] / 16;
-    if (chunks == 0)
-      continue;
-    const u32x4* src = reinterpret_cast<const u32x4*>(p.prefetch[r]);
-    for (unsigned long long c = static_cast<unsigned long long>(group) * blockDim.x + threadIdx.x;
-         c < chunks; c += kInFlight * stride) {
-      u32x4 v[kInFlight];
-#pragma unroll
-      for (int k = 0; k < kInFlight; ++k)
-        v[k] = src[min(c + k * stride, chunks - 1)];
-#pragma unroll
-      for (int k = 0; k < kInFlight; ++k)
-        fold ^= v[k].x;
-    }
-  }
-  // Never true (prefetch_groups > 0 here); keeps the loads alive.
-  if (fold == 0x9e3779b9u && p.prefetch_groups < 0)
-    p.out[0] = static_cast<half_t>(0.0F);
-}
-
 template <int GROUP>
 __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
     AttentionParams p) {
   if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
-    PrefetchRanges(p, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
+    PrefetchWeights(p.prefetch, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
     return;
   }
   constexpr int kWaves = 4 * GROUP;  // compute waves; wave kWaves: producer
@@ -429,7 +400,7 @@ constexpr int ExactLds() {
 template <int GROUP, int MAXR>
 __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
-    PrefetchRanges(p, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
+    PrefetchWeights(p.prefetch, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
     return;
   }
   extern __shared__ __align__(16) unsigned char lds[];
@@ -688,7 +659,7 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
           "multiple of 16");
   const int group = p.heads / p.kv_heads;
   Require(group == 1 || group == 2, "attention: query heads per kv head must be 1 or 2");
-  Require(p.prefetch_groups >= 0, "attention: negative prefetch group count");
+  Require(p.prefetch.groups >= 0, "attention: negative prefetch group count");
   Require(p.exact_count >= 0 && p.exact_count <= p.work_count,
           "attention: exact work count outside the work list");
   Require(p.exact_count == 0 ||
@@ -701,7 +672,7 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
   if (p.exact_count > 0) {
     AttentionParams e = p;
     e.work_count = p.exact_count;
-    const dim3 grid(e.work_count * e.kv_heads + e.prefetch_groups);
+    const dim3 grid(e.work_count * e.kv_heads + e.prefetch.groups);
     auto launch = [&](auto kernel, int lds_bytes) {
       Dispatch(kernel, grid, dim3(256), lds_bytes, stream, true, !online, e);
     };
@@ -725,8 +696,8 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
     AttentionParams l = p;
     l.work = p.work + p.exact_count;
     l.work_count = p.work_count - p.exact_count;
-    l.prefetch_groups = p.exact_count > 0 ? 0 : p.prefetch_groups;
-    const dim3 grid(l.work_count * l.kv_heads + l.prefetch_groups);
+    l.prefetch.groups = p.exact_count > 0 ? 0 : p.prefetch.groups;
+    const dim3 grid(l.work_count * l.kv_heads + l.prefetch.groups);
     if (group == 1)
       Dispatch(AttentionKernel<1>, grid, dim3(5 * 64), AttentionLds<1>(), stream,
                p.exact_count == 0, true, l);

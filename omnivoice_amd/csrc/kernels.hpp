@@ -184,6 +184,45 @@ void LaunchRmsNorm(const float* x, const int* gather, const float* w,
 // With `gather` null, src = r and h is written back to hidden[r]; with
 // `gather` set, src = gather[r] and hidden is left untouched (the final
 // norm of the target rows).
+// Weight prefetch: `groups` extra work-groups after the attention's own
+// read these byte ranges (the weights of the GEMMs that follow), so that
+// those GEMMs find them in the memory-side cache instead of HBM. Nothing is
+// stored.
+struct WeightPrefetch {
+  static constexpr int kMaxRanges = 5;
+  const unsigned char* range[kMaxRanges];
+  unsigned long long bytes[kMaxRanges];
+  int groups;
+};
+
+// The prefetch work-group `group` (0 .. w.groups - 1): each thread keeps
+// eight 16-byte loads in flight (clamped in bounds, no load under a
+// condition) and folds them into a value that only an empty asm statement
+// consumes, so only the cache fill remains.
+__device__ __forceinline__ void PrefetchWeights(const WeightPrefetch& w, int group) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kInFlight = 8;
+  const unsigned long long stride = static_cast<unsigned long long>(w.groups) * blockDim.x;
+  unsigned int fold = 0;
+  for (int r = 0; r < WeightPrefetch::kMaxRanges; ++r) {
+    const unsigned long long chunks = w.bytes[r] / 16;
+    if (chunks == 0)
+      continue;
+    const u32x4* src = reinterpret_cast<const u32x4*>(w.range[r]);
+    for (unsigned long long c = static_cast<unsigned long long>(group) * blockDim.x + threadIdx.x;
+         c < chunks; c += kInFlight * stride) {
+      u32x4 v[kInFlight];
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        v[k] = src[min(c + k * stride, chunks - 1)];
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        fold ^= v[k].x;
+    }
+  }
+  asm volatile("" : : "v"(fold));
+}
+
 struct AddNormParams {
   float* hidden;             // [rows][width]
   const float* partials;     // splits slices of [rows][width]
@@ -223,13 +262,7 @@ struct AttentionParams {
   int work_count;
   int ld_qk, ldvt, heads, kv_heads;
   float scale_log2;        // log2(e) / sqrt(128)
-  // Weight prefetch: `prefetch_groups` extra work-groups after the attention
-  // ones read these byte ranges (the weights of the GEMMs that follow), so
-  // that those GEMMs find them in the memory-side cache instead of HBM.
-  static constexpr int kMaxPrefetch = 5;
-  const unsigned char* prefetch[kMaxPrefetch];
-  unsigned long long prefetch_bytes[kMaxPrefetch];
-  int prefetch_groups;
+  WeightPrefetch prefetch;
   // work[0, exact_count): sequences of at most kExactAttentionKeys keys,
   // whose scores fit in registers (two-pass softmax, at most exact_rounds
   // rounds of four 32-key tiles); the rest take the online-softmax kernel.

@@ -16,7 +16,7 @@
 //    device table through a counter the embedding kernel advances.
 //  * The Gumbel noise stream (std::mt19937_64, decoding.cpp:83-86) is drawn
 //    on the host for every executed step up front and uploaded once.
-//  * Several inputs can share one packed batch (sequences aligned to 8 rows).
+//  * Several inputs can share one packed batch (sequences aligned to 16 rows).
 //  * The text embedding table lives in HBM (the reference keeps it mmapped on
 //    the host and gathers rows per request, generator.cpp:206-217).
 #include <hip/hip_runtime.h>
@@ -25,6 +25,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <string>
@@ -38,6 +39,19 @@
 
 namespace ovg {
 namespace {
+
+void SetPrefetch(WeightPrefetch& w, std::initializer_list<const DeviceBuffer<half_t>*> ranges,
+                 int groups) {
+  Require(ranges.size() <= WeightPrefetch::kMaxRanges, "prefetch: too many ranges");
+  w = WeightPrefetch{};
+  int r = 0;
+  for (const DeviceBuffer<half_t>* b : ranges) {
+    w.range[r] = reinterpret_cast<const unsigned char*>(b->get());
+    w.bytes[r] = b->bytes();
+    ++r;
+  }
+  w.groups = groups;
+}
 
 struct Layer {
   DeviceBuffer<half_t> qkv;      // [(heads + 2 kv) * 128][hidden]
@@ -701,6 +715,13 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     Run(prof, name, 0.0, static_cast<double>(rows) * H * (4.0 * (splits + 2) + 2.0),
         [&] { LaunchAddNorm(a, stream_); });
   };
+  // Weight prefetch only where the attention keeps at most 96 work-groups
+  // busy (the 2 s shape: 40): with more, the reads outlast the attention and
+  // delay everything after it (10 s shape, 152 work-groups: 535 vs 544
+  // unmask steps/s with and without a 31.5 MB prefetch in the attention;
+  // clone and chunk shapes likewise, measured).
+  const int attention_busy = static_cast<int>(L.work.size()) * static_cast<int>(cfg_.kv_heads);
+  const bool prefetch = attention_busy <= 96;
   const int o_splits = PlanPacked(M, H, heads_width, Epilogue::kPartial).splits;
   const int down_splits = PlanPacked(M, H, I, Epilogue::kPartial).splits;
   for (std::size_t l = 0; l < layers_.size(); ++l) {
@@ -718,28 +739,24 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
            p.kv_heads = static_cast<int>(cfg_.kv_heads);
            p.eps = cfg_.rms_norm_eps;
          });
-    // The attention leaves CUs idle (one work-group per query tile and kv
-    // head): extra work-groups pull this layer's o, gate/up and down weights
-    // and the next layer's q/k/v (after the last layer: the audio heads and
-    // layer 0's q/k/v) into the memory-side cache, from which the GEMMs then
-    // stream them.
-    {
-      const Layer& next = layers_[(l + 1) % layers_.size()];
-      const DeviceBuffer<half_t>* ranges[AttentionParams::kMaxPrefetch] = {
-          &W.output, &W.gate_up, &W.down, l + 1 < layers_.size() ? &next.qkv : &heads_,
-          l + 1 < layers_.size() ? nullptr : &next.qkv};
-      for (int r = 0; r < AttentionParams::kMaxPrefetch; ++r) {
-        ap.prefetch[r] = ranges[r] ? reinterpret_cast<const unsigned char*>(ranges[r]->get())
-                                   : nullptr;
-        ap.prefetch_bytes[r] = ranges[r] ? ranges[r]->bytes() : 0;
-      }
-      // Only where most CUs would idle (the 2 s shape: 40 attention
-      // work-groups): with fewer prefetch work-groups the 31.5 MB outlast
-      // the attention and delay everything after it (10 s shape, 152
-      // work-groups: 535 vs 544 unmask steps/s with and without; clone and
-      // chunk shapes likewise, measured).
-      const int busy = ap.work_count * ap.kv_heads;
-      ap.prefetch_groups = busy <= 96 ? 256 - busy : 0;
+    // The attention leaves CUs idle at short utterances (one work-group per
+    // query tile and kv head): there, extra work-groups pull this layer's o,
+    // gate/up and down weights and the next layer's q/k/v (after the last
+    // layer: the audio heads and layer 0's q/k/v) into the memory-side
+    // cache, from which the GEMMs then stream them. (Moving the down and
+    // q/k/v parts into the add + norm launches, which leave CUs idle there
+    // too, shortened the attention but made each add + norm wait for its
+    // prefetch: 857 vs 870 unmask steps/s at 2 s, same box.)
+    const Layer& next = layers_[(l + 1) % layers_.size()];
+    const bool last_layer = l + 1 == layers_.size();
+    ap.prefetch = WeightPrefetch{};
+    if (prefetch) {
+      if (last_layer)
+        SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down, &heads_, &next.qkv},
+                    256 - attention_busy);
+      else
+        SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down, &next.qkv},
+                    256 - attention_busy);
     }
     Run(prof, "attention", attention_flops, R * (qkv_n + heads_width) * 2.0,
         [&] { LaunchAttention(ap, stream_); });
@@ -762,9 +779,8 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
            p.ldc = H;
            p.split_stride = part_stride;
          });
-    if (l + 1 < layers_.size())
-      add_norm("add_norm", down_splits, layers_[l + 1].input_norm.get(),
-               normed_.get(), nullptr, M);
+    if (!last_layer)
+      add_norm("add_norm", down_splits, next.input_norm.get(), normed_.get(), nullptr, M);
     else  // GatherRows + final RmsNorm (generator.cpp:295-298)
       add_norm("add_norm_final", down_splits, final_norm_.get(),
                final_normed_.get(), gather_.get(), L.targets);

@@ -291,21 +291,21 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
         }
       }
     } else if (live && slot >= 0) {
-      // Value head gv: V^T element (gv, d, row) at VtIndex, d the head
+      // Value head: the head's staging area holds it as [dim 128][row 32 XB]
+      // fp16, rows in VtColumn order inside each 16-row block, so that the
+      // 8 keys of one V^T chunk are 16 consecutive bytes; d is the head
       // column of the element (rope order inside the block).
-      const int gv = slot - p.heads - p.kv_heads;
 #pragma unroll
       for (int wb = 0; wb < WB; ++wb) {
         const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
 #pragma unroll
         for (int b = 0; b < XB; ++b) {
-          const int m = m0 + 32 * b + col;
-          if (m >= p.m)
-            continue;
+          const int r_local = VtColumn(32 * b + col);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
-            p.vt[VtIndex(gv, d, m, p.ldvt)] = static_cast<half_t>(acc[wb][b][r]);
+            *reinterpret_cast<half_t*>(lds + stage + (d * kBM + r_local) * 2) =
+                static_cast<half_t>(acc[wb][b][r]);
           }
         }
       }
@@ -327,6 +327,26 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
             *reinterpret_cast<const half8*>(lds + stage + r * 256 + ((q ^ (r & 15)) << 4));
         if (m < p.m)
           *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m, 8 * q, p.ldq)) = v;
+      }
+    } else if (live && slot >= 0) {
+      // The 4 / WB waves of this value head copy its staged V^T out in
+      // 16-byte chunks (VtIndex): chunk (16-row block, dim group, half,
+      // dim 32) holds 8 keys of one dim; 32 lanes store 512 consecutive
+      // bytes. Blocks past the last row are not written (a partial last
+      // block is, with finite values from the clamped operand rows).
+      const int gv = slot - p.heads - p.kv_heads;
+      constexpr int kLanes = 64 * (4 / WB);
+      const int t = (wave % (4 / WB)) * 64 + lane;
+#pragma unroll
+      for (int pass = 0; pass < 2 * XB * 256 / kLanes; ++pass) {
+        const int e = pass * kLanes + t;
+        const int d32 = e & 31, half = (e >> 5) & 1, dt = (e >> 6) & 3, b16 = e >> 8;
+        const int d = 32 * dt + d32;
+        const half8 v = *reinterpret_cast<const half8*>(
+            lds + stage + (d * kBM + 16 * b16 + 8 * half) * 2);
+        if (m0 + 16 * b16 < p.m)
+          *reinterpret_cast<half8*>(p.vt + VtIndex(gv, d, m0 + 16 * b16 + (half ? 4 : 0),
+                                                   p.ldvt)) = v;
       }
     }
   }

@@ -363,13 +363,14 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // rescaled while keys stream, and the key quarters' partial outputs merge
 // as a plain sum.
 //
-// One work-group per (32-query tile, kv head) with four waves, one per
-// SIMD: wave q takes key tiles q, q + 4, q + 8, ... for all GROUP query
-// heads of the kv head, so every K and V^T operand byte is used by exactly
-// one wave and goes from memory straight into registers (QkIndex and
-// VtIndex store each 32-row tile's operands as whole 256-byte runs), as do
-// the query operands (read by all four waves, from L2): the LDS holds only
-// the softmax statistics and the final merge. A wave's tiles stream through a ring of
+// One work-group per (32-query tile, kv head) with 4 x GROUP / HPW waves:
+// wave w takes key tiles q, q + 4, q + 8, ... (q = w % 4) for HPW of the
+// GROUP query heads of the kv head. Every K and V^T operand goes from
+// memory straight into registers (QkIndex and
+// VtIndex store each 32-row tile's operands as whole 256-byte runs; with
+// HPW = GROUP each operand byte is used by exactly one wave, with HPW = 1
+// the waves of one quarter load the same tiles), as do the query operands:
+// the LDS holds only the softmax statistics and the final merge. A wave's tiles stream through a ring of
 // operand buffers, one or two tiles ahead: its key tiles, then its value
 // tiles, so the first value tiles load while the softmax runs. Every load
 // is unconditional (a slot past the wave's last tile re-reads a tile of the
@@ -397,8 +398,8 @@ constexpr int ExactLds() {
   return stats > merge ? stats : merge;
 }
 
-template <int GROUP, int MAXR>
-__global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
+template <int GROUP, int MAXR, int HPW>
+__global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(AttentionParams p) {
   if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
     PrefetchWeights(p.prefetch, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
     return;
@@ -407,7 +408,9 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   const int g = blockIdx.x % p.kv_heads;
   const AttentionWork work = p.work[blockIdx.x / p.kv_heads];
   const int lane = threadIdx.x & 63;
-  const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quarter = wave % kRound;
+  const int head0 = (wave / kRound) * HPW;  // this wave's first head of the group
   const int half_id = lane >> 5;
   const int col = lane & 31;
   const int tiles = (work.seq_length + kKTile - 1) / kKTile;
@@ -447,10 +450,10 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   // The query tiles' operands straight into registers (rows past the
   // tile's count belong to the next rows; their results are never stored),
   // then the first operand slots.
-  half8 qf[GROUP][8];
+  half8 qf[HPW][8];
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h) {
-    const half_t* q_tile = p.qk + static_cast<size_t>(g * GROUP + h) * p.ld_qk +
+  for (int h = 0; h < HPW; ++h) {
+    const half_t* q_tile = p.qk + static_cast<size_t>(g * GROUP + head0 + h) * p.ld_qk +
                            static_cast<size_t>(work.q_begin >> 4) * 2048;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
@@ -464,7 +467,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   // Key phase: S^T = K Q^T per tile and head, unscaled; lane holds keys
   // 8 (e / 4) + 4 half_id + e % 4 of its query column. Keys past the
   // sequence (only in its last, partial tile) are -inf.
-  floatx16 s[GROUP][MAXR];
+  floatx16 s[HPW][MAXR];
   auto key_tile = [&](auto jc) {
     constexpr int j = decltype(jc)::value;
     if constexpr (j + kDepth - 1 < 2 * MAXR)
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
     if (j < mine) {
       const int valid_keys = work.seq_length - (kRound * j + quarter) * kKTile;
 #pragma unroll
-      for (int h = 0; h < GROUP; ++h) {
+      for (int h = 0; h < HPW; ++h) {
         floatx16 acc = floatx16{};
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
@@ -494,11 +497,11 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   // so the maximum of the unscaled scores serves), then p = fp16(e / sum).
   float* smax = reinterpret_cast<float*>(lds);
   float* ssum = smax + GROUP * kRound * 32;
-  float inverse[GROUP];
+  float inverse[HPW];
   {
-    float m[GROUP];
+    float m[HPW];
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
+    for (int h = 0; h < HPW; ++h) {
       m[h] = -__builtin_inff();
 #pragma unroll
       for (int j = 0; j < MAXR; ++j)
@@ -508,13 +511,13 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
             m[h] = fmaxf(m[h], s[h][j][e]);
       m[h] = fmaxf(m[h], __shfl_xor(m[h], 32));
       if (half_id == 0)
-        smax[(h * kRound + quarter) * 32 + col] = m[h];
+        smax[((head0 + h) * kRound + quarter) * 32 + col] = m[h];
     }
     RingBarrier();
-    float sum[GROUP];
+    float sum[HPW];
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
-      const float* hm = smax + h * kRound * 32 + col;
+    for (int h = 0; h < HPW; ++h) {
+      const float* hm = smax + (head0 + h) * kRound * 32 + col;
       const float shift = -(fmaxf(fmaxf(hm[0], hm[32]), fmaxf(hm[64], hm[96])) * p.scale_log2);
       sum[h] = 0.0F;
 #pragma unroll
@@ -527,21 +530,21 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
           }
       sum[h] += __shfl_xor(sum[h], 32);
       if (half_id == 0)
-        ssum[(h * kRound + quarter) * 32 + col] = sum[h];
+        ssum[((head0 + h) * kRound + quarter) * 32 + col] = sum[h];
     }
     RingBarrier();
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
-      const float* hs = ssum + h * kRound * 32 + col;
+    for (int h = 0; h < HPW; ++h) {
+      const float* hs = ssum + (head0 + h) * kRound * 32 + col;
       inverse[h] = 1.0F / ((hs[0] + hs[32]) + (hs[64] + hs[96]));
     }
   }
   // P^T operand for keys 16 j2 .. 16 j2 + 15 of a tile: slot e is
   // accumulator element 8 j2 + e; VtIndex puts the same keys in the chunk
   // of lane half half_id.
-  half8 pf[GROUP][MAXR][2];
+  half8 pf[HPW][MAXR][2];
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h)
+  for (int h = 0; h < HPW; ++h)
 #pragma unroll
     for (int j = 0; j < MAXR; ++j)
       if (j < mine)
@@ -552,9 +555,9 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
             pf[h][j][j2][e] = static_cast<half_t>(s[h][j][8 * j2 + e] * inverse[h]);
 
   // Value phase: O^T = V^T P^T over this quarter's tiles, every head.
-  floatx16 o[GROUP][4];
+  floatx16 o[HPW][4];
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h)
+  for (int h = 0; h < HPW; ++h)
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
       o[h][dt] = floatx16{};
@@ -569,7 +572,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-          for (int h = 0; h < GROUP; ++h)
+          for (int h = 0; h < HPW; ++h)
             o[h][dt] = Mfma32(buf[slot % kDepth][2 * dt + j2], pf[h][j][j2], o[h][dt]);
     }
   };
@@ -582,7 +585,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   floatx4* accs = reinterpret_cast<floatx4*>(lds);
   RingBarrier();
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h)
+  for (int h = 0; h < HPW; ++h)
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       if (dt == quarter)
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
       const int part = dt < quarter ? dt : dt - 1;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        accs[(((quarter * 3 + part) * GROUP + h) * 4 + k) * 64 + lane] =
+        accs[(((quarter * 3 + part) * GROUP + head0 + h) * 4 + k) * 64 + lane] =
             floatx4{o[h][dt][4 * k], o[h][dt][4 * k + 1], o[h][dt][4 * k + 2],
                     o[h][dt][4 * k + 3]};
     }
@@ -598,7 +601,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
   if (col >= work.q_count)
     return;
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h) {
+  for (int h = 0; h < HPW; ++h) {
     const floatx16 own = quarter == 0   ? o[h][0]
                          : quarter == 1 ? o[h][1]
                          : quarter == 2 ? o[h][2]
@@ -610,7 +613,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
       floatx16 v;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const floatx4 x = accs[(((q * 3 + part) * GROUP + h) * 4 + k) * 64 + lane];
+        const floatx4 x = accs[(((q * 3 + part) * GROUP + head0 + h) * 4 + k) * 64 + lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           v[4 * k + i] = x[i];
@@ -619,7 +622,7 @@ __global__ __launch_bounds__(256) void ExactAttentionKernel(AttentionParams p) {
     };
     const floatx16 result = (load(0) + load(1)) + (load(2) + load(3));
     half_t* out = p.out + static_cast<size_t>(work.q_begin + col) * p.heads * kHeadDim +
-                  (g * GROUP + h) * kHeadDim + quarter * 32;
+                  (g * GROUP + head0 + h) * kHeadDim + quarter * 32;
     // Lane holds dims 8 (e / 4) + 4 half_id + e % 4 of the slice.
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -673,23 +676,30 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
     AttentionParams e = p;
     e.work_count = p.exact_count;
     const dim3 grid(e.work_count * e.kv_heads + e.prefetch.groups);
-    auto launch = [&](auto kernel, int lds_bytes) {
-      Dispatch(kernel, grid, dim3(256), lds_bytes, stream, true, !online, e);
+    // Up to four tiles per wave: two waves per SIMD, one query head each,
+    // so that one wave's softmax overlaps the other's MFMAs and loads (the
+    // two heads' waves of a quarter load the same operands, close enough
+    // in time to meet in L1); with five or six, one wave per SIMD doing
+    // both heads of the group, whose registers fit the longer score block
+    // (10 s: 8.5 vs 9.1 us, 2 s: 8.8 vs 9.0, clone: 20.7 vs 20.0, same
+    // box). A query's arithmetic is the same either way.
+    auto launch = [&](auto kernel, int waves, int lds_bytes) {
+      Dispatch(kernel, grid, dim3(64 * waves), lds_bytes, stream, true, !online, e);
     };
     // The kernel instance holds exactly the largest per-wave tile count.
     switch (group * 8 + p.exact_rounds) {
-      case 9: launch(ExactAttentionKernel<1, 1>, ExactLds<1>()); break;
-      case 10: launch(ExactAttentionKernel<1, 2>, ExactLds<1>()); break;
-      case 11: launch(ExactAttentionKernel<1, 3>, ExactLds<1>()); break;
-      case 12: launch(ExactAttentionKernel<1, 4>, ExactLds<1>()); break;
-      case 13: launch(ExactAttentionKernel<1, 5>, ExactLds<1>()); break;
-      case 14: launch(ExactAttentionKernel<1, 6>, ExactLds<1>()); break;
-      case 17: launch(ExactAttentionKernel<2, 1>, ExactLds<2>()); break;
-      case 18: launch(ExactAttentionKernel<2, 2>, ExactLds<2>()); break;
-      case 19: launch(ExactAttentionKernel<2, 3>, ExactLds<2>()); break;
-      case 20: launch(ExactAttentionKernel<2, 4>, ExactLds<2>()); break;
-      case 21: launch(ExactAttentionKernel<2, 5>, ExactLds<2>()); break;
-      default: launch(ExactAttentionKernel<2, 6>, ExactLds<2>()); break;
+      case 9: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1>()); break;
+      case 10: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1>()); break;
+      case 11: launch(ExactAttentionKernel<1, 3, 1>, 4, ExactLds<1>()); break;
+      case 12: launch(ExactAttentionKernel<1, 4, 1>, 4, ExactLds<1>()); break;
+      case 13: launch(ExactAttentionKernel<1, 5, 1>, 4, ExactLds<1>()); break;
+      case 14: launch(ExactAttentionKernel<1, 6, 1>, 4, ExactLds<1>()); break;
+      case 17: launch(ExactAttentionKernel<2, 1, 1>, 8, ExactLds<2>()); break;
+      case 18: launch(ExactAttentionKernel<2, 2, 1>, 8, ExactLds<2>()); break;
+      case 19: launch(ExactAttentionKernel<2, 3, 1>, 8, ExactLds<2>()); break;
+      case 20: launch(ExactAttentionKernel<2, 4, 1>, 8, ExactLds<2>()); break;
+      case 21: launch(ExactAttentionKernel<2, 5, 2>, 4, ExactLds<2>()); break;
+      default: launch(ExactAttentionKernel<2, 6, 2>, 4, ExactLds<2>()); break;
     }
   }
   if (online) {

@@ -225,6 +225,34 @@ def test_attention_matches_oracle(seqs):
         assert to_rounded < to_exact
 
 
+@pytest.mark.parametrize("heads,kv,seqs", [
+    (8, 8, [(0, 100), (112, 700)]),      # one query head per kv head
+    (16, 8, [(0, 768), (768, 769)]),     # the last exact length, the first online one
+    (16, 8, [(0, 16), (16, 48), (64, 20)]),  # several short sequences, 16-row starts
+])
+def test_attention_head_groups_and_limits(heads, kv, seqs):
+    """The attention against the oracle for one query head per kv head, at
+    the 768-key limit of the exact kernel and one key past it, and for
+    several short packed sequences."""
+    rng = np.random.default_rng(heads + seqs[-1][1])
+    rows = seqs[-1][0] + seqs[-1][1]
+    width = (heads + 2 * kv) * 128
+    qkv = (rng.standard_normal((rows, width)) * 1.5).astype(np.float16)
+    out = torch.zeros((rows, heads * 128), dtype=torch.float16, device="cuda")
+    ov.op_attention(dev(qkv), out, heads, kv, seqs)
+    s = np.array(seqs, dtype=np.int64).ravel()
+    q32 = qkv.astype(np.float32)
+    want = np.zeros((rows, heads * 128), dtype=np.float32)
+    oracle.lib().orc_attention(q32.ctypes.data, want.ctypes.data, rows, heads,
+                               kv, 128, s.ctypes.data, len(seqs), 1)
+    got = host(out).astype(np.float32)
+    for first, length in seqs:
+        sl = slice(first, first + length)
+        err = np.abs(got[sl] - want[sl]).max()
+        rel = np.linalg.norm(got[sl] - want[sl]) / np.linalg.norm(want[sl])
+        assert err < 1.5e-2 and rel < 3e-3, (length, err, rel)
+
+
 def test_attention_batch_invariant():
     """A sequence's attention output does not depend on what else is packed
     beside it: alone (one round of keys held in registers) and packed after

@@ -2,10 +2,16 @@
 // matrix cores: replaces State::Attention's two batched GEMMs, the
 // materialised [heads][L][L] scores, SoftmaxKernel and MergeHeadsKernel of
 // the reference (generator.cpp:122-172, kernels/generator_kernels.hip:
-// 161-189). Scores never leave registers.
+// 161-189). Scores never leave registers. Two kernels; which one a query
+// takes depends on its own sequence's length only (PlanAttentionWork):
+//  * ExactAttentionKernel, sequences of at most 768 keys (every shape of
+//    the generator's workloads): the reference's exact softmax, operands
+//    straight from memory into registers; described at the kernel below.
+//  * AttentionKernel, longer sequences: online softmax over LDS-staged
+//    tiles, described next.
 //
-// A work-group takes one tile of 32 queries of one sequence and one key/value
-// head g, with 4 x GROUP waves (the GROUP query heads of g times four key
+// AttentionKernel: a work-group takes one tile of 32 queries of one
+// sequence and one key/value head g, with 4 x GROUP waves (the GROUP query heads of g times four key
 // quarters). Keys come in 32-key tiles (K [32][128] and V^T 2 x [128][16],
 // 16 KB), fetched global -> LDS by DMA into an 8-slot ring, four tiles (a
 // round) at a time, quarter q taking tile 4 r + q of round r. The queries

@@ -715,13 +715,17 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     Run(prof, name, 0.0, static_cast<double>(rows) * H * (4.0 * (splits + 2) + 2.0),
         [&] { LaunchAddNorm(a, stream_); });
   };
-  // Weight prefetch only where the attention keeps at most 96 work-groups
-  // busy (the 2 s shape: 40): with more, the reads outlast the attention and
-  // delay everything after it (10 s shape, 152 work-groups: 535 vs 544
-  // unmask steps/s with and without a 31.5 MB prefetch in the attention;
-  // clone and chunk shapes likewise, measured).
+  // How much weight the attention launch prefetches depends on how many
+  // CUs it leaves idle. At most 96 busy work-groups (the 2 s shape: 40): the
+  // four GEMMs that follow, 31.5 MB. At most 160 (the 10 s shape: 152): only
+  // this layer's o, gate/up and down, 22 MB, which the idle CUs read within
+  // about the attention's own time (all four: 535 vs 544 unmask steps/s
+  // without; these three: 555 vs 546, o and gate/up alone 552, same boxes).
+  // With more (clone, chunks) the reads outlast the attention and delay
+  // everything after it: none.
   const int attention_busy = static_cast<int>(L.work.size()) * static_cast<int>(cfg_.kv_heads);
   const bool prefetch = attention_busy <= 96;
+  const bool prefetch_near = !prefetch && attention_busy <= 160;
   const int o_splits = PlanPacked(M, H, heads_width, Epilogue::kPartial).splits;
   const int down_splits = PlanPacked(M, H, I, Epilogue::kPartial).splits;
   for (std::size_t l = 0; l < layers_.size(); ++l) {
@@ -750,7 +754,9 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     const Layer& next = layers_[(l + 1) % layers_.size()];
     const bool last_layer = l + 1 == layers_.size();
     ap.prefetch = WeightPrefetch{};
-    if (prefetch) {
+    if (prefetch_near) {
+      SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down}, 256 - attention_busy);
+    } else if (prefetch) {
       if (last_layer)
         SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down, &heads_, &next.qkv},
                     256 - attention_busy);

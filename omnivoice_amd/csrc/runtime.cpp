@@ -745,9 +745,12 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
          });
     // The attention leaves CUs idle at short utterances (one work-group per
     // query tile and kv head): there, extra work-groups pull this layer's o,
-    // gate/up and down weights and the next layer's q/k/v (after the last
-    // layer: the audio heads and layer 0's q/k/v) into the memory-side
-    // cache, from which the GEMMs then stream them. (Moving the down and
+    // gate/up and down weights, and at the shortest also the next layer's
+    // q/k/v (after the last layer: the audio heads and layer 0's q/k/v),
+    // into the memory-side cache, from which the GEMMs then stream them.
+    // (Prefetch work-groups in the GEMM launches instead, on the CUs their
+    // tiles leave free, slowed those GEMMs: 10 s 515 vs 545 unmask steps/s,
+    // same box. Moving the down and
     // q/k/v parts into the add + norm launches, which leave CUs idle there
     // too, shortened the attention but made each add + norm wait for its
     // prefetch: 857 vs 870 unmask steps/s at 2 s, same box.)

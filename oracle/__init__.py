@@ -104,6 +104,7 @@ def lib() -> ctypes.CDLL:
         "orc_qk_norm_rope": (None, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
                                     _f32, _f32]),
         "orc_attention": (None, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, ctypes.c_int]),
+        "orc_swiglu": (None, [_ptr, _ptr, _i64, _i64]),
         "orc_snake": (None, [_ptr, _i64, _i64, _ptr, _ptr]),
         "orc_conv1d": (None, [_ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr]),
         "orc_conv_transpose1d": (None, [_ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _ptr]),

@@ -229,6 +229,18 @@ void AttentionRows(const float* qkv, float* out, int64_t rows, int64_t heads,
   }
 }
 
+// kernels::SwiGlu: silu(gate) * up, gate = columns [0, inter) and up =
+// [inter, 2 inter) of each row (kernels/generator_kernels.hip:191-200).
+void SwiGluRows(const float* gate_up, float* out, int64_t rows, int64_t inter) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t i = 0; i < inter; ++i) {
+      const float g = gate_up[r * 2 * inter + i];
+      const float u = gate_up[r * 2 * inter + inter + i];
+      out[r * inter + i] = g / (1.0F + std::exp(-g)) * u;
+    }
+}
+
 struct Layer {
   std::vector<float> qkv;      // [q rows | k rows | v rows][hidden]
   std::vector<float> output;   // [hidden][heads * d]
@@ -398,6 +410,10 @@ void orc_attention(const float* qkv, float* out, int64_t rows, int64_t heads,
                 round_p != 0);
 }
 
+void orc_swiglu(const float* gate_up, float* out, int64_t rows, int64_t inter) {
+  SwiGluRows(gate_up, out, rows, inter);
+}
+
 // Generator::Forward: the packed CFG batch of one ConditionalInput (cond
 // rows [0, length), then its last target_frames again as the unconditional
 // sequence), the layers, and the audio heads on the 2F target rows.
@@ -469,14 +485,7 @@ void orc_forward(void* handle, const int32_t* ids, int64_t length,
     RoundAll(normed.data(), rows * h, em);
     Gemm(normed.data(), L.gate_up.data(), gate_up.data(), rows, h, 2 * in,
          false);
-#pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < rows; ++r)
-      for (int64_t i = 0; i < in; ++i) {
-        const float g = gate_up[static_cast<std::size_t>(r * 2 * in + i)];
-        const float u = gate_up[static_cast<std::size_t>(r * 2 * in + in + i)];
-        activated[static_cast<std::size_t>(r * in + i)] =
-            g / (1.0F + std::exp(-g)) * u;
-      }
+    SwiGluRows(gate_up.data(), activated.data(), rows, in);
     RoundAll(activated.data(), rows * in, em);
     Gemm(activated.data(), L.down.data(), hidden.data(), rows, in, h, true);
   }

@@ -17,7 +17,13 @@
  *   orc_exp / orc_log    - glibc expf/logf within 2 ulp over sweeps.
  *   orc_score            - float64 closed form per row; invariants.
  *   orc_forward pieces   - float64 textbook formulas at tiny shapes and the
- *                          installed transformers Qwen3 layer (fixtures).
+ *                          installed transformers Qwen3 layer (fixtures);
+ *                          orc_swiglu against float64; orc_attention's
+ *                          rounded probabilities against float64 with fp16 P.
+ *   orc_forward emulate  - bit for bit the composition of the pinned pieces
+ *                          rounding (orc_round_half, pinned against numpy's
+ *                          float16) at exactly the reference's seven fp16
+ *                          points; dropping any one changes the bits.
  *   orc_synth_*          - numpy float16 rounding; closed-form moments.
  *   orc_model_from_host  - the synthetic model's tensors in the reference's
  *                          load layout give the synthetic model's logits bit
@@ -129,6 +135,7 @@ void orc_qk_norm_rope(const float* qkv, const float* q_norm,
 void orc_attention(const float* qkv, float* out, int64_t rows, int64_t heads,
                    int64_t kv_heads, int64_t head_dim,
                    const int64_t* sequences, int64_t count, int round_p);
+void orc_swiglu(const float* gate_up, float* out, int64_t rows, int64_t inter);
 
 /* codec.cpp: the audio decoder (codec.cpp:197-260 of the reference) */
 typedef struct orc_codec_config {

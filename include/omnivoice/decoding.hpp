@@ -19,7 +19,7 @@ struct DecodingConfig {
   float guidance = 2.0F;
   float t_shift = 0.1F;
   float layer_penalty = 5.0F;
-  /// Gumbel noise on the position scores; 0 selects positions greedily.
+  /// Temperature of the Gumbel-perturbed position choice (0 = greedy).
   float position_temperature = 5.0F;
 };
 
@@ -35,10 +35,11 @@ struct ConditionalInput {
   std::size_t length = 0;
   std::size_t audio_start = 0;
   std::size_t target_frames = 0;
-  /// [codebook][position].
+  /// Row-major ids, one row of `length` per codebook.
   std::vector<std::int32_t> ids;
 
-  /// `reference_codes` is [codebook][frame] (reference decoding.cpp:42-62).
+  /// Lays out text ids, the reference codes (one row of `reference_frames`
+  /// per codebook) and masked target frames (reference decoding.cpp:42-62).
   [[nodiscard]] static ConditionalInput Build(
       const std::vector<std::uint32_t>& text_ids,
       const std::vector<std::int32_t>& reference_codes,
@@ -47,9 +48,9 @@ struct ConditionalInput {
 };
 
 struct GenerationResult {
-  /// [codebook][frame].
+  /// Final codes, one row of target frames per codebook.
   std::vector<std::int32_t> codes;
-  /// The step that unmasked each code, [codebook][frame].
+  /// Per code, the index of the step at which it was chosen (same layout).
   std::vector<std::int32_t> unmasked_at;
 };
 
@@ -58,8 +59,9 @@ class PositionSelector {
  public:
   PositionSelector(const DecodingConfig& config, std::uint64_t seed);
 
-  /// `codes`, `prediction` and `confidence` are [codebook][frame]; returns
-  /// the flat indices it filled, best first.
+  /// Fills the `count` best masked entries of `codes` with their
+  /// predictions (all three arrays hold one row of frames per codebook) and
+  /// returns their flat indices in rank order.
   std::vector<std::size_t> Fill(std::size_t count, std::size_t codebooks,
                                 std::size_t frames,
                                 const std::vector<std::int32_t>& prediction,

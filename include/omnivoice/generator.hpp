@@ -21,8 +21,10 @@ namespace gufo::models::omnivoice {
 class Generator {
  public:
   /// Reference generator.hpp:22-24: reads model_root/model.safetensors (the
-  /// checkpoint's float32 tensors). An empty `model_root` builds the seeded
-  /// synthetic model (weight seed 1234) instead.
+  /// checkpoint's float32 tensors). An empty `model_root` names
+  /// model.safetensors in the working directory and fails, as the
+  /// reference's Load does, when it is absent; synthetic weights come only
+  /// from LoadSynthetic.
   [[nodiscard]] static std::unique_ptr<Generator> Load(
       const Config& config, const std::filesystem::path& model_root,
       std::string* error = nullptr);

@@ -301,7 +301,9 @@ int ovg_op_linear(const void* x, const void* w, float* y, int64_t rows,
  * did not would be rejected with an error. Same kernels and plan as
  * ovg_op_linear, so the same result bit for bit; enqueued on `stream`
  * without waiting for it. Calls that overlap on one GPU (two streams or two
- * threads) share the array and race: serialise them. */
+ * threads) share the array and race: serialise them. The first call on each
+ * GPU looks up that GPU's address of the array (hipGetSymbolAddress); make it
+ * outside graph capture, after which calls may be captured and replayed. */
 #define OVG_LINEAR_NOALLOC_SCRATCH_FLOATS 1048576
 int ovg_op_linear_noalloc(const void* x, const void* w, float* y, int64_t rows,
                           int64_t in, int64_t out, int accumulate, void* stream,

@@ -17,6 +17,11 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
+// MI355X: 8 XCDs of 32 compute units; a launch's work-groups are dealt to
+// the XCDs in turn (work-group i to XCD i % 8).
+constexpr int kXcds = 8;
+constexpr int kCus = 256;
+
 // Each packed sequence starts at a multiple of this many rows, so that its
 // 32-row tiles are two whole 16-row blocks of the attention's operand
 // layouts (QkIndex, VtIndex).

@@ -25,8 +25,9 @@ class DeviceBuffer {
 
   // Grows to `count` elements (contents are lost, new memory is zeroed);
   // returns true when it reallocated. The zeroing runs on the null stream,
-  // which work on a non-blocking stream does not wait for, so it is waited
-  // for here: otherwise it could land after that work's first writes.
+  // which work on a non-blocking stream does not wait for, so the null
+  // stream is waited for here (and only it, not the other engines' streams):
+  // otherwise the zeroing could land after that work's first writes.
   bool Reserve(std::size_t count) {
     if (count <= count_)
       return false;
@@ -36,7 +37,7 @@ class DeviceBuffer {
           "hipMalloc");
     Check(hipMemset(data_, 0, std::max<std::size_t>(count, 1) * sizeof(T)),
           "hipMemset");
-    Check(hipDeviceSynchronize(), "hipMemset");
+    Check(hipStreamSynchronize(nullptr), "hipMemset");
     count_ = count;
     return true;
   }

@@ -49,8 +49,6 @@ namespace {
 
 constexpr int kBN = 128;
 constexpr int kBK = 64;
-constexpr int kXcds = 8;
-constexpr int kCus = 256;  // MI355X: 8 XCDs x 32 CUs
 constexpr int kBBytes = kBN * kBK * 2;  // one stage of B: 16 KB
 
 // FM = 32-row MFMA blocks per wave strip. Eight waves in two K groups of

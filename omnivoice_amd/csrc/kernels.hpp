@@ -65,8 +65,7 @@ enum class Epilogue : int {
   kAccumulate = 1,  // y fp32 [M][ldc] += acc (the residual stream)
   kQkvRope = 2,     // per-head RMSNorm + rotary for q/k heads -> fp16
                     // qk at QkIndex(head, row, d, ldq); v heads ->
-                    // fp16 V^T at VtIndex
-                    // vt[g][d][VtColumn(row)] (ldvt % 16 == 0)
+                    // fp16 V^T at VtIndex (ldvt % 16 == 0)
   kSwiGlu = 3,      // act fp16 [M][ldh] = silu(gate) * up; the W rows pair
                     // gate and up rows: per 128-row tile 64 gate rows then
                     // the matching 64 up rows (GemmKernel), or per packed
@@ -146,6 +145,9 @@ std::size_t PackedWeightHalves(int rows, int k);
 // heads per kv head) on the device.
 void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
                  half_t* out, hipStream_t stream);
+// The same from a float32 source, rounded to fp16 on the device.
+void PackWeights(const float* w, const float* w2, int rows, int k, PackMap map, int group,
+                 half_t* out, hipStream_t stream);
 struct PackedPlan {
   int xb = 4;      // tile height in 32-row blocks (1-4, or 8 with wb 2)
   int wb = 1;      // tile width in 128-column units (2: 128 x 256 or 256 x 256)
@@ -178,12 +180,6 @@ void LaunchRmsNorm(const float* x, const int* gather, const float* w,
                    half_t* out, int rows, int width, float eps,
                    hipStream_t stream);
 
-// The residual update and the next RMSNorm in one pass over rows:
-//   h = hidden[src] + partial[0][src] + partial[1][src] + ... (that order)
-//   out[r] = half(norm * h * rsqrt(mean(h^2) + eps))
-// With `gather` null, src = r and h is written back to hidden[r]; with
-// `gather` set, src = gather[r] and hidden is left untouched (the final
-// norm of the target rows).
 // Weight prefetch: `groups` extra work-groups after the attention's own
 // read these byte ranges (the weights of the GEMMs that follow), so that
 // those GEMMs find them in the memory-side cache instead of HBM. Nothing is
@@ -223,6 +219,12 @@ __device__ __forceinline__ void PrefetchWeights(const WeightPrefetch& w, int gro
   asm volatile("" : : "v"(fold));
 }
 
+// The residual update and the next RMSNorm in one pass over rows:
+//   h = hidden[src] + partial[0][src] + partial[1][src] + ... (that order)
+//   out[r] = half(norm * h * rsqrt(mean(h^2) + eps))
+// With `gather` null, src = r and h is written back to hidden[r]; with
+// `gather` set, src = gather[r] and hidden is left untouched (the final
+// norm of the target rows).
 struct AddNormParams {
   float* hidden;             // [rows][width]
   const float* partials;     // splits slices of [rows][width]

@@ -63,8 +63,6 @@
 namespace ovg {
 namespace {
 
-constexpr int kXcds = 8;
-constexpr int kCus = 256;
 
 template <int XB>
 struct Packed {
@@ -916,10 +914,13 @@ void PackedBigKernel(GemmParams p, int tiles_m, int k_steps) {
                             wave * kHeadStage<XB>);
 }
 
-// Packs row-major fp16 W [rows][K] into the fragment order above: half8
+// Packs row-major W [rows][K] into the fragment order above: half8
 // number ((block K/64 + t) 4 + j) 64 + l holds W[row(block, l % 32)][64 t +
 // 32 (l / 32) + 8 j .. + 7]; rows past `rows` are zero. One thread per half8.
-__global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, int k,
+// A float32 source is rounded to fp16 here (round to nearest even, as the
+// reference's ConvertToHalf does on the host, generator.cpp:31-49).
+template <typename T>
+__global__ void PackWeightsKernel(const T* w, const T* w2, int rows, int k,
                                   int blocks, PackMap map, int group, half8* out) {
   const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
   const size_t o = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -931,7 +932,7 @@ __global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, i
   const int t = static_cast<int>(bt % (k / 64));
   const int block = static_cast<int>(bt / (k / 64));
   const int i = lane & 31;
-  const half_t* src = w;
+  const T* src = w;
   int row = 32 * block + i;
   if (map == PackMap::kRope) {
     const int wv = block % 4;
@@ -943,9 +944,20 @@ __global__ void PackWeightsKernel(const half_t* w, const half_t* w2, int rows, i
     src = i < 16 ? w : w2;
   }
   half8 v = {};
-  if (row < rows)
-    v = *reinterpret_cast<const half8*>(src + static_cast<size_t>(row) * k + 64 * t +
-                                        32 * (lane >> 5) + 8 * j);
+  if (row < rows) {
+    const T* p = src + static_cast<size_t>(row) * k + 64 * t + 32 * (lane >> 5) + 8 * j;
+    if constexpr (sizeof(T) == 2) {
+      v = *reinterpret_cast<const half8*>(p);
+    } else {
+      const floatx4 lo = *reinterpret_cast<const floatx4*>(p);
+      const floatx4 hi = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = static_cast<half_t>(lo[e]);
+        v[4 + e] = static_cast<half_t>(hi[e]);
+      }
+    }
+  }
   out[o] = v;
 }
 
@@ -1007,8 +1019,9 @@ std::size_t PackedWeightHalves(int rows, int k) {
   return static_cast<std::size_t>((rows + 255) / 256 * 256) * k;
 }
 
-void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
-                 half_t* out, hipStream_t stream) {
+template <typename T>
+void PackWeightsAny(const T* w, const T* w2, int rows, int k, PackMap map, int group,
+                    half_t* out, hipStream_t stream) {
   Require(k % 64 == 0 && rows > 0, "pack: K must be a positive multiple of 64");
   Require(map != PackMap::kRope || (group > 0 && rows % 128 == 0 && (rows / 128) % (group + 2) == 0),
           "pack: q/k/v packing needs (group + 2) kv groups of 128-row heads");
@@ -1018,9 +1031,20 @@ void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map
   const int blocks = (out_rows + 255) / 256 * 8;
   const size_t total = static_cast<size_t>(blocks) * (k / 64) * 256;
   const int threads = 256;
-  PackWeightsKernel<<<static_cast<unsigned>((total + threads - 1) / threads), threads, 0,
-                      stream>>>(w, w2, rows, k, blocks, map, group, reinterpret_cast<half8*>(out));
+  PackWeightsKernel<T><<<static_cast<unsigned>((total + threads - 1) / threads), threads, 0,
+                         stream>>>(w, w2, rows, k, blocks, map, group,
+                                   reinterpret_cast<half8*>(out));
   Check(hipGetLastError(), "pack launch");
+}
+
+void PackWeights(const half_t* w, const half_t* w2, int rows, int k, PackMap map, int group,
+                 half_t* out, hipStream_t stream) {
+  PackWeightsAny(w, w2, rows, k, map, group, out, stream);
+}
+
+void PackWeights(const float* w, const float* w2, int rows, int k, PackMap map, int group,
+                 half_t* out, hipStream_t stream) {
+  PackWeightsAny(w, w2, rows, k, map, group, out, stream);
 }
 
 PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {

@@ -56,7 +56,7 @@ void SetPrefetch(WeightPrefetch& w, std::initializer_list<const DeviceBuffer<hal
 struct Layer {
   DeviceBuffer<half_t> qkv;      // [(heads + 2 kv) * 128][hidden]
   DeviceBuffer<half_t> output;   // [hidden][heads * 128]
-  DeviceBuffer<half_t> gate_up;  // 128-row tiles: 64 gate rows, 64 up rows
+  DeviceBuffer<half_t> gate_up;  // packed blocks of 16 gate + 16 up rows (PackMap::kSwiGlu)
   DeviceBuffer<half_t> down;     // [hidden][intermediate]
   DeviceBuffer<float> input_norm, post_norm, q_norm, k_norm;
 };
@@ -131,6 +131,14 @@ class Engine {
   void LoadSynthetic(std::uint64_t seed, float jitter);
   void UploadPacked(DeviceBuffer<half_t>& dst, const std::vector<half_t>& host, int rows,
                     int k, PackMap map);
+  // Float32 host pieces, concatenated on the device in the given order,
+  // rounded to fp16 and packed there.
+  struct HostPiece {
+    const float* data;
+    std::size_t count;
+  };
+  void UploadPackedFloat(DeviceBuffer<half_t>& dst, const std::vector<HostPiece>& pieces,
+                         int rows, int k, PackMap map);
   void LoadHost(const ovg_host_weights& w);
   std::int64_t DeviceBytes() const;
 
@@ -260,6 +268,32 @@ void Engine::UploadPacked(DeviceBuffer<half_t>& dst, const std::vector<half_t>& 
   Check(hipStreamSynchronize(stream_), "pack weights");
 }
 
+void Engine::UploadPackedFloat(DeviceBuffer<half_t>& dst, const std::vector<HostPiece>& pieces,
+                               int rows, int k, PackMap map) {
+  std::size_t total = 0;
+  for (const HostPiece& piece : pieces) {
+    Require(piece.data != nullptr, "missing host tensor");
+    total += piece.count;
+  }
+  const int out_rows = map == PackMap::kSwiGlu ? 2 * rows : rows;
+  Require(total == static_cast<std::size_t>(out_rows) * k, "host tensor sizes");
+  DeviceBuffer<float> staging;
+  staging.Reserve(total);
+  std::size_t offset = 0;
+  for (const HostPiece& piece : pieces) {
+    Check(hipMemcpyAsync(staging.get() + offset, piece.data, piece.count * sizeof(float),
+                         hipMemcpyHostToDevice, stream_),
+          "upload weights");
+    offset += piece.count;
+  }
+  dst.Reserve(PackedWeightHalves(out_rows, k));
+  PackWeights(staging.get(),
+              map == PackMap::kSwiGlu ? staging.get() + static_cast<std::size_t>(rows) * k
+                                      : nullptr,
+              rows, k, map, static_cast<int>(cfg_.heads / cfg_.kv_heads), dst.get(), stream_);
+  Check(hipStreamSynchronize(stream_), "pack weights");
+}
+
 void Engine::LoadSynthetic(std::uint64_t seed, float jitter) {
   const std::size_t h = static_cast<std::size_t>(cfg_.hidden_size);
   const std::size_t inter = static_cast<std::size_t>(cfg_.intermediate_size);
@@ -371,45 +405,31 @@ void Engine::LoadHost(const ovg_host_weights& w) {
     Check(hipMemcpy(b.get(), src, n * sizeof(float), hipMemcpyHostToDevice),
           "upload weights");
   };
-  auto to_half = [](const float* src, std::size_t n, half_t* dst) {
-    Require(src != nullptr, "missing host tensor");
-    ParallelChunks(n, [&](std::size_t b, std::size_t e) {
-      for (std::size_t i = b; i < e; ++i)
-        dst[i] = ToHalf(src[i]);
-    });
-  };
+  // The matrices go to the device as float32 and are rounded to fp16 there,
+  // while being packed (the reference converts on the host,
+  // generator.cpp:31-49, with the same rounding).
   upload_float(text_, w.text_embeddings,
                static_cast<std::size_t>(cfg_.vocab_size) * h);
   upload_float(audio_, w.audio_embeddings, audio_rows * h);
   upload_float(final_norm_, w.final_norm, h);
-  std::vector<half_t> matrix(audio_rows * h, static_cast<half_t>(0.0F));
-  to_half(w.audio_heads, audio_rows * h, matrix.data());
-  UploadPacked(heads_, matrix, static_cast<int>(audio_rows), static_cast<int>(h),
-               PackMap::kIdentity);
+  UploadPackedFloat(heads_, {{w.audio_heads, audio_rows * h}}, static_cast<int>(audio_rows),
+                    static_cast<int>(h), PackMap::kIdentity);
   layers_ = std::vector<Layer>(static_cast<std::size_t>(cfg_.layers));
   for (std::int64_t l = 0; l < cfg_.layers; ++l) {
     const float* const* t = w.layers + l * OVG_LAYER_TENSORS;
     Layer& L = layers_[static_cast<std::size_t>(l)];
-    matrix.assign((q_rows + 2 * kv_rows) * h, static_cast<half_t>(0.0F));
-    to_half(t[OVG_LAYER_Q_PROJ], q_rows * h, matrix.data());
-    to_half(t[OVG_LAYER_K_PROJ], kv_rows * h, matrix.data() + q_rows * h);
-    to_half(t[OVG_LAYER_V_PROJ], kv_rows * h,
-            matrix.data() + (q_rows + kv_rows) * h);
-    UploadPacked(L.qkv, matrix, static_cast<int>(q_rows + 2 * kv_rows), static_cast<int>(h),
-                 PackMap::kRope);
-    matrix.assign(h * q_rows, static_cast<half_t>(0.0F));
-    to_half(t[OVG_LAYER_O_PROJ], h * q_rows, matrix.data());
-    UploadPacked(L.output, matrix, static_cast<int>(h), static_cast<int>(q_rows),
-                 PackMap::kIdentity);
-    matrix.assign(2 * inter * h, static_cast<half_t>(0.0F));
-    to_half(t[OVG_LAYER_GATE_PROJ], inter * h, matrix.data());
-    to_half(t[OVG_LAYER_UP_PROJ], inter * h, matrix.data() + inter * h);
-    UploadPacked(L.gate_up, matrix, static_cast<int>(inter), static_cast<int>(h),
-                 PackMap::kSwiGlu);
-    matrix.assign(h * inter, static_cast<half_t>(0.0F));
-    to_half(t[OVG_LAYER_DOWN_PROJ], h * inter, matrix.data());
-    UploadPacked(L.down, matrix, static_cast<int>(h), static_cast<int>(inter),
-                 PackMap::kIdentity);
+    UploadPackedFloat(L.qkv,
+                      {{t[OVG_LAYER_Q_PROJ], q_rows * h},
+                       {t[OVG_LAYER_K_PROJ], kv_rows * h},
+                       {t[OVG_LAYER_V_PROJ], kv_rows * h}},
+                      static_cast<int>(q_rows + 2 * kv_rows), static_cast<int>(h), PackMap::kRope);
+    UploadPackedFloat(L.output, {{t[OVG_LAYER_O_PROJ], h * q_rows}}, static_cast<int>(h),
+                      static_cast<int>(q_rows), PackMap::kIdentity);
+    UploadPackedFloat(L.gate_up,
+                      {{t[OVG_LAYER_GATE_PROJ], inter * h}, {t[OVG_LAYER_UP_PROJ], inter * h}},
+                      static_cast<int>(inter), static_cast<int>(h), PackMap::kSwiGlu);
+    UploadPackedFloat(L.down, {{t[OVG_LAYER_DOWN_PROJ], h * inter}}, static_cast<int>(h),
+                      static_cast<int>(inter), PackMap::kIdentity);
     upload_float(L.input_norm, t[OVG_LAYER_INPUT_NORM], h);
     upload_float(L.post_norm, t[OVG_LAYER_POST_NORM], h);
     upload_float(L.q_norm, t[OVG_LAYER_Q_NORM], 128);
@@ -758,14 +778,14 @@ void Engine::EnqueueForward(const Layout& L, Profiler* prof) {
     const bool last_layer = l + 1 == layers_.size();
     ap.prefetch = WeightPrefetch{};
     if (prefetch_near) {
-      SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down}, 256 - attention_busy);
+      SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down}, kCus - attention_busy);
     } else if (prefetch) {
       if (last_layer)
         SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down, &heads_, &next.qkv},
-                    256 - attention_busy);
+                    kCus - attention_busy);
       else
         SetPrefetch(ap.prefetch, {&W.output, &W.gate_up, &W.down, &next.qkv},
-                    256 - attention_busy);
+                    kCus - attention_busy);
     }
     Run(prof, "attention", attention_flops, R * (qkv_n + heads_width) * 2.0,
         [&] { LaunchAttention(ap, stream_); });

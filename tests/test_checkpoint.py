@@ -117,3 +117,72 @@ def test_checkpoint_matches_synthetic_model(tiny_config, tmp_path):
     r1 = loaded.generate(x, ov.DecodingConfig(), 7)
     r2 = synthetic.generate(x, ov.DecodingConfig(), 7)
     assert (r1.codes == r2.codes).all() and (r1.unmasked_at == r2.unmasked_at).all()
+
+
+def random_checkpoint(cfg, seed):
+    """Float32 tensors under the checkpoint's names whose values are not
+    fp16-exact (N(0, 0.02) matrices and embeddings, norms around 1)."""
+    rng = np.random.default_rng(seed)
+    dims = {"h": cfg["hidden_size"], "i": cfg["intermediate_size"],
+            "q": cfg["heads"] * cfg["head_dim"], "kv": cfg["kv_heads"] * cfg["head_dim"],
+            "d": cfg["head_dim"]}
+    audio_rows = cfg["audio_codebooks"] * cfg["audio_vocab_size"]
+    h = cfg["hidden_size"]
+
+    def draw(shape, norm=False):
+        x = 1.0 + 0.1 * rng.standard_normal(shape) if norm else 0.02 * rng.standard_normal(shape)
+        return x.astype(np.float32)
+
+    out = {"llm.embed_tokens.weight": draw((cfg["vocab_size"], h)),
+           "audio_embeddings.weight": draw((audio_rows, h)),
+           "audio_heads.weight": draw((audio_rows, h)),
+           "llm.norm.weight": draw((h,), True)}
+    for layer in range(cfg["layers"]):
+        for name, rows, cols, _, norm in LAYER_TENSORS:
+            shape = (dims[rows], dims[cols]) if cols else (dims[rows],)
+            out[f"llm.layers.{layer}.{name}"] = draw(shape, norm)
+    return out
+
+
+def oracle_host(cfg, tensors):
+    """The same tensors in the oracle's host layout (the reference's Load
+    order, generator.cpp:377-425)."""
+    return {"text": tensors["llm.embed_tokens.weight"],
+            "audio_embeddings": tensors["audio_embeddings.weight"],
+            "audio_heads": tensors["audio_heads.weight"],
+            "final_norm": tensors["llm.norm.weight"],
+            "layers": [[tensors[f"llm.layers.{layer}.{name}"] for name, *_ in LAYER_TENSORS]
+                       for layer in range(cfg["layers"])]}
+
+
+@pytest.mark.gpu
+def test_checkpoint_of_arbitrary_values_matches_oracle(tiny_config, tmp_path):
+    """A checkpoint of float32 values that fp16 cannot hold exactly: the
+    matrices are rounded to fp16 on the GPU while being packed, as the
+    reference's ConvertToHalf rounds them on the host (generator.cpp:31-49,
+    364-434), so the loaded model's logits are within the parity bound of the
+    float32 oracle built from the same tensors (which rounds its matrices the
+    same way), and identical to the same tensors given through the host
+    entry point."""
+    import oracle
+    tensors = random_checkpoint(tiny_config, 5)
+    assert any((t != t.astype(np.float16).astype(np.float32)).any()
+               for t in tensors.values())
+    write(tmp_path, tensors)
+    loaded = ov.Generator.load(tiny_config, str(tmp_path))
+    host = oracle_host(tiny_config, tensors)
+    model = oracle.Model(tiny_config, host=host)
+    from_host = ov.Generator.from_host(tiny_config, host)
+    rng = np.random.default_rng(9)
+    for text, target in [(9, 30), (23, 61)]:
+        x = ov.ConditionalInput.build(rng.integers(0, tiny_config["vocab_size"], size=text),
+                                      None, 0, target)
+        got = loaded.forward(x)
+        want = model.forward(x.ids, text, target)
+        rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+        print(f"({text}, {target}): max-abs {np.abs(got - want).max():.3e} rel-l2 {rel:.3e}")
+        assert np.abs(got - want).max() < 2e-2
+        assert rel < 1e-3
+        assert got.tobytes() == from_host.forward(x).tobytes()
+    loaded.close()
+    from_host.close()

@@ -227,6 +227,7 @@ def test_attention_matches_oracle(seqs):
 
 @pytest.mark.parametrize("heads,kv,seqs", [
     (8, 8, [(0, 100), (112, 700)]),      # one query head per kv head
+    (8, 8, [(0, 800), (816, 100)]),      # one query head per kv head, online and exact
     (16, 8, [(0, 768), (768, 769)]),     # the last exact length, the first online one
     (16, 8, [(0, 16), (16, 48), (64, 20)]),  # several short sequences, 16-row starts
 ])

@@ -41,3 +41,38 @@ def test_linear_noalloc_matches_linear(torch):
         assert torch.equal(got, want), (rows, k, n)
         ref = x.float() @ w.float().t() + (y0 if acc else 0)
         assert torch.allclose(got, ref, rtol=1e-3, atol=1e-3)
+
+
+def test_linear_noalloc_captured_in_a_graph(torch):
+    """After a first eager call on the device (which looks up the array's
+    address), the entry point captured in a graph on a side stream replays
+    to ovg_op_linear's result bit for bit, replay after replay, with other
+    eager work between the replays."""
+    gen = torch.Generator().manual_seed(12)
+    rows, k, n = 40, 2048, 512  # 32-row tiles in 8 K-splits: the array is used
+    x = (torch.randn(rows, k, generator=gen) * 0.5).half().cuda()
+    w = (torch.randn(n, k, generator=gen) * 0.05).half().cuda()
+    want = torch.empty(rows, n, device="cuda")
+    ov.op_linear(x, w, want)
+    warm = torch.empty(rows, n, device="cuda")
+    ov.op_linear_noalloc(x, w, warm)
+    torch.cuda.synchronize()
+    assert torch.equal(warm, want)
+    got = torch.empty(rows, n, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            ov.op_linear_noalloc(x, w, got, stream=side)
+    torch.cuda.current_stream().wait_stream(side)
+    other = (torch.randn(rows, k, generator=gen) * 0.5).half().cuda()
+    for replay in range(3):
+        got.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), replay
+        # Eager work on the same array between replays.
+        scratch_user = torch.empty(rows, n, device="cuda")
+        ov.op_linear_noalloc(other, w, scratch_user)
+        torch.cuda.synchronize()

@@ -416,11 +416,6 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   half8 wf[4][4];       // W of steps t .. t + 3, slot t % 4
   half8 xs[2][XB];      // X of steps t + 2 and t + 3, slot t % 2
   half8 fr[2][4][XB];   // fragments of X(t) (slot t % 2) and X(t + 1)
-  auto load_w = [&](half8 (&dst)[4], int t) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      dst[j] = w_src[(t * 4 + j) * 64];
-  };
   auto load_x = [&](half8 (&dst)[XB], int t) {
 #pragma unroll
     for (int i = 0; i < XB; ++i)
@@ -444,23 +439,28 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   // load makes the compiler's wait counts assume it was skipped and wait for
   // the loads before it.
   //
-  // The loads are issued in the loop's own order (X of a step, then W of
-  // that step), so that at the loop's first step the loads in flight are
-  // those of its steady state: the compiler's wait counts at the loop head
-  // are the smaller of what the first iteration and the later ones need, and
-  // a prologue in another order made two steps in four wait for loads issued
-  // one step earlier instead of two.
+  // The loads are issued in the loop's own order (W of a step's first three
+  // substeps, X of the step, W of its last substep), so that at the loop's
+  // first step the loads in flight are those of its steady state: the
+  // compiler's wait counts at the loop head are the smaller of what the
+  // first iteration and the later ones need, and a prologue in another order
+  // made two steps in four wait for loads issued one step earlier instead of
+  // two.
   const int last = steps - 1;
   {
     half8 x0[XB], x1[XB];
-    load_w(wf[0], 0);
-    load_w(wf[1], min(1, last));
-    load_x(x0, 0);
-    load_x(x1, min(1, last));
-    load_x(xs[0], min(2, last));
-    load_w(wf[2], min(2, last));
-    load_x(xs[1], min(3, last));
-    load_w(wf[3], min(3, last));
+    auto load_step = [&](int s, half8 (&x)[XB]) {
+      const int t = min(s, last);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        wf[s][j] = w_src[(t * 4 + j) * 64];
+      load_x(x, t);
+      wf[s][3] = w_src[(t * 4 + 3) * 64];
+    };
+    load_step(0, x0);
+    load_step(1, x1);
+    load_step(2, xs[0]);
+    load_step(3, xs[1]);
     store_x(x0, 0);
     store_x(x1, 1);
   }
@@ -473,15 +473,16 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   // 4 XB MFMAs of step t from fragments already in registers, each followed
   // by memory work of the step, so that it issues in the MFMA's shadow (with
   // one wave per SIMD an MFMA holds up the wave's next instruction for its 32
-  // clocks): first, one per row block, the write of X(t + 2) into buffer
-  // (t + 2) % 4 (its previous content, X(t - 2), was last read in step
-  // t - 3) and the reload of those registers with X(t + 4); after every
-  // MFMA one read of X(t + 1)'s fragments from buffer (t + 1) % 4 (written in
-  // step t - 1, before the barrier that ended it), so no MFMA waits for LDS;
-  // after a substep's last MFMA the reload of its W slot with W(t + 4). The
-  // step ends at a barrier that first waits for all of its LDS operations,
-  // after which X(t + 2) is readable. (Letting the fragment reads run on
-  // across the barrier measured no faster.)
+  // clocks): after every MFMA one read of X(t + 1)'s fragments from buffer
+  // (t + 1) % 4 (written in step t - 1, before the barrier that ended it), so
+  // no MFMA waits for LDS; after a substep's last MFMA the reload of its W
+  // slot with W(t + 4); in the last substep, one per row block, the write of
+  // X(t + 2) into buffer (t + 2) % 4 (its previous content, X(t - 2), was
+  // last read in step t - 3) and the reload of those registers with X(t + 4).
+  // The step ends at a barrier that first waits for all of its LDS
+  // operations, after which X(t + 2) is readable. (Writing X(t + 2) in the
+  // first substep instead measured 1-3 % slower at 580 rows; letting the
+  // fragment reads run on across the barrier measured no faster.)
   auto step = [&](int t, auto slot) {
     constexpr int ws = decltype(slot)::value;  // t % 4
     constexpr int xo = ws & 1;                 // t % 2
@@ -492,10 +493,11 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
       acc[0][b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[0][b])
                             : Mfma32(fr[xo][j][b], wf[ws][j], acc[0][b]);
       __builtin_amdgcn_sched_barrier(0);
-      if (i < XB) {
-        *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[i]) = xs[xo][i];
+      if (i >= 3 * XB) {
+        const int xi = i - 3 * XB;
+        *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) = xs[xo][xi];
         AsmFence();
-        xs[xo][i] = x_src[i][ahead * 8];
+        xs[xo][xi] = x_src[xi][ahead * 8];
       }
       fr[1 - xo][i / XB][i % XB] = *reinterpret_cast<const half8*>(
           lds + ((ws + 1) & 3) * S::kStageBytes + x_read[i % XB][i / XB]);

@@ -597,13 +597,6 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   half8 wf[2][WB][4];  // W of steps t, t + 1, slot t % 2
   half8 xs[2][XB];     // X of steps t + 2 and t + 3, slot t % 2
   half8 fr[2][XB];     // X fragments of the current and the next substep
-  auto load_w = [&](half8 (&dst)[WB][4], int t) {
-#pragma unroll
-    for (int wb = 0; wb < WB; ++wb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        dst[wb][j] = w_src[wb * w_next + (t * 4 + j) * 64];
-  };
   auto load_x = [&](half8 (&dst)[XB], int t) {
 #pragma unroll
     for (int i = 0; i < XB; ++i)
@@ -623,18 +616,28 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   // Prologue: W of steps 0 and 1, X of steps 0 .. 3 (X(0), X(1) to LDS
   // buffers 0 and 1), then the fragments of step 0's first substep. Step
   // indices past the last are clamped (in-bounds reloads never used).
-  // Loads in the loop's own order (X of step t + 4, then W of step t + 2),
-  // so that the compiler's wait counts at the loop head are those of the
-  // steady state.
+  // Loads in the loop's own order (W of step t + 2's first three substeps,
+  // X of step t + 4, W of step t + 2's last substep), so that the
+  // compiler's wait counts at the loop head are those of the steady state.
   const int last = steps - 1;
   {
     half8 x0[XB], x1[XB];
     load_x(x0, 0);
     load_x(x1, min(1, last));
-    load_x(xs[0], min(2, last));
-    load_w(wf[0], 0);
-    load_x(xs[1], min(3, last));
-    load_w(wf[1], min(1, last));
+    auto load_step = [&](int s, half8 (&x)[XB]) {
+      const int t = min(s, last);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int wb = 0; wb < WB; ++wb)
+          wf[s][wb][j] = w_src[wb * w_next + (t * 4 + j) * 64];
+      load_x(x, min(s + 2, last));
+#pragma unroll
+      for (int wb = 0; wb < WB; ++wb)
+        wf[s][wb][3] = w_src[wb * w_next + (t * 4 + 3) * 64];
+    };
+    load_step(0, xs[0]);
+    load_step(1, xs[1]);
     store_x(x0, 0);
     store_x(x1, 1);
   }
@@ -647,7 +650,7 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
   // next instruction for its 32 clocks): after every other MFMA one read of
   // the next substep's fragments (substep j + 1 of buffer t % 4, or the
   // first substep of step t + 1 from buffer (t + 1) % 4, written in step
-  // t - 1); in substep 0, after the others, the write of X(t + 2) into LDS
+  // t - 1); in substep 3, after the others, the write of X(t + 2) into LDS
   // buffer (t + 2) % 4 and the reload of those registers with X(t + 4);
   // after the last MFMA of a W fragment its reload with W(t + 2). The step
   // ends at a barrier that waits for all of its LDS operations. A buffer is
@@ -670,7 +673,7 @@ __global__ __launch_bounds__(256) void PackedWideKernel(GemmParams p, int tiles_
           const int buf = j < 3 ? ws : (ws + 1) & 3;
           fr[(j + 1) & 1][rb] = *reinterpret_cast<const half8*>(
               lds + buf * S::kStageBytes + x_read[rb][j < 3 ? j + 1 : 0]);
-        } else if (j == 0) {
+        } else if (j == 3) {
           const int xi = i / 2;
           *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) =
               xs[xo][xi];

@@ -123,6 +123,8 @@ class Engine {
     graphs_.clear();
     if (stream_ != nullptr)
       (void)hipStreamDestroy(stream_);
+    if (noise_host_ != nullptr)
+      (void)hipHostFree(noise_host_);
   }
 
   const ovg_config& config() const { return cfg_; }
@@ -181,6 +183,11 @@ class Engine {
   void UploadDecodingPlan(const Layout& L, const ovg_decoding& d,
                           const std::vector<std::uint64_t>& seeds,
                           std::vector<int>* launch_steps);
+  // Draws the Gumbel noise of executed step k (every item's positions, in
+  // the item's own mt19937_64 stream) into pinned host memory and enqueues
+  // its copy to the device ahead of that step's kernels, so that the host
+  // draws step k + 1's noise while the GPU runs step k.
+  void EnqueueNoise(std::size_t k);
   GraphEntry* StepGraph(const Layout& L, const ovg_decoding& d);
 
   template <typename T>
@@ -217,6 +224,15 @@ class Engine {
   DeviceBuffer<SelectStep> plan_;
 
   std::map<std::string, std::unique_ptr<GraphEntry>> graphs_;
+
+  // The decoding plan of the current call and its noise streams: executed
+  // step k's noise is [noise_begin_[k], noise_begin_[k + 1]) of noise_ (and
+  // of the pinned staging noise_host_), items in order.
+  std::vector<SelectStep> plan_host_;
+  std::vector<std::mt19937_64> noise_random_;
+  std::vector<std::size_t> noise_total_, noise_begin_;
+  float* noise_host_ = nullptr;
+  std::size_t noise_host_count_ = 0;
 };
 
 // ------------------------------------------------------------------ weights
@@ -885,38 +901,71 @@ void Engine::UploadDecodingPlan(const Layout& L, const ovg_decoding& d,
     if (any)
       launch_steps->push_back(static_cast<int>(s));
   }
+  // Step-major noise offsets: executed step k's noise, all items, is one
+  // contiguous range, drawn and uploaded just before step k (EnqueueNoise).
   const bool noisy = d.position_temperature > 0.0F;
-  std::vector<SelectStep> plan(launch_steps->size() * items);
-  std::vector<float> noise;
-  for (std::size_t i = 0; i < items; ++i) {
-    std::mt19937_64 random(seeds[i]);
-    const std::size_t total = C * static_cast<std::size_t>(L.items[i].frames);
-    for (std::size_t k = 0; k < launch_steps->size(); ++k) {
-      const int step = (*launch_steps)[k];
-      SelectStep& st = plan[k * items + i];
+  const std::size_t executed = launch_steps->size();
+  plan_host_.assign(executed * items, SelectStep{});
+  noise_total_.assign(items, 0);
+  noise_begin_.assign(executed + 1, 0);
+  std::size_t running = 0;
+  for (std::size_t k = 0; k < executed; ++k) {
+    noise_begin_[k] = running;
+    const int step = (*launch_steps)[k];
+    for (std::size_t i = 0; i < items; ++i) {
+      const std::size_t total = C * static_cast<std::size_t>(L.items[i].frames);
+      noise_total_[i] = total;
+      SelectStep& st = plan_host_[k * items + i];
       st.step = step;
       st.count = static_cast<int>(schedules[i][static_cast<std::size_t>(step)]);
       st.noise_offset = 0;
       if (noisy && st.count > 0) {
-        st.noise_offset = static_cast<int>(noise.size());
-        noise.resize(noise.size() + total);
-        GumbelNoise(&random, total, noise.data() + st.noise_offset);
+        st.noise_offset = static_cast<int>(running);
+        running += total;
       }
     }
   }
-  Grow(plan_, std::max<std::size_t>(plan.size(), 1));
-  Grow(noise_, std::max<std::size_t>(noise.size(), 1));
-  if (!plan.empty())
-    Check(hipMemcpyAsync(plan_.get(), plan.data(),
-                         plan.size() * sizeof(SelectStep),
+  noise_begin_[executed] = running;
+  Require(running < (std::size_t{1} << 31), "noise plan too large");
+  noise_random_.clear();
+  for (std::size_t i = 0; i < items; ++i)
+    noise_random_.emplace_back(seeds[i]);
+  // Every entry point waits for its stream before it returns, so no copy
+  // from the previous staging buffer is pending here.
+  if (running > noise_host_count_) {
+    if (noise_host_ != nullptr)
+      Check(hipHostFree(noise_host_), "hipHostFree");
+    noise_host_ = nullptr;
+    noise_host_count_ = 0;
+    Check(hipHostMalloc(reinterpret_cast<void**>(&noise_host_), running * sizeof(float),
+                        hipHostMallocDefault),
+          "hipHostMalloc");
+    noise_host_count_ = running;
+  }
+  Grow(plan_, std::max<std::size_t>(plan_host_.size(), 1));
+  Grow(noise_, std::max<std::size_t>(running, 1));
+  if (!plan_host_.empty())
+    Check(hipMemcpyAsync(plan_.get(), plan_host_.data(),
+                         plan_host_.size() * sizeof(SelectStep),
                          hipMemcpyHostToDevice, stream_),
           "upload step plan");
-  if (!noise.empty())
-    Check(hipMemcpyAsync(noise_.get(), noise.data(),
-                         noise.size() * sizeof(float), hipMemcpyHostToDevice,
-                         stream_),
-          "upload noise");
-  Check(hipStreamSynchronize(stream_), "upload step plan");
+}
+
+void Engine::EnqueueNoise(std::size_t k) {
+  Require(k + 1 < noise_begin_.size(), "noise step outside the plan");
+  const std::size_t begin = noise_begin_[k], end = noise_begin_[k + 1];
+  if (end == begin)
+    return;
+  const std::size_t items = noise_random_.size();
+  for (std::size_t i = 0; i < items; ++i) {
+    const SelectStep& st = plan_host_[k * items + i];
+    if (st.count > 0)
+      GumbelNoise(&noise_random_[i], noise_total_[i],
+                  noise_host_ + static_cast<std::size_t>(st.noise_offset));
+  }
+  Check(hipMemcpyAsync(noise_.get() + begin, noise_host_ + begin, (end - begin) * sizeof(float),
+                       hipMemcpyHostToDevice, stream_),
+        "upload noise");
 }
 
 Engine::GraphEntry* Engine::StepGraph(const Layout& L, const ovg_decoding& d) {
@@ -1011,6 +1060,7 @@ int Engine::Generate(const std::vector<Input>& inputs, const ovg_decoding& d,
         status = OVG_CANCELLED;
         break;
       }
+      EnqueueNoise(k);
       Check(hipGraphLaunch(graph->exec, stream_), "hipGraphLaunch");
       Check(hipEventRecord(done[k % 2], stream_), "hipEventRecord");
     }
@@ -1073,7 +1123,9 @@ void Engine::GenerateTrace(const std::vector<Input>& inputs, const ovg_decoding&
     schedules.push_back(UnmaskSchedule(C * static_cast<std::size_t>(it.frames),
                                        static_cast<std::size_t>(d.steps), d.t_shift));
   executed->assign(L.items.size(), 0);
-  for (const int step : launch_steps) {
+  for (std::size_t k = 0; k < launch_steps.size(); ++k) {
+    const int step = launch_steps[k];
+    EnqueueNoise(k);
     EnqueueForward(L, nullptr);
     EnqueueScore(L, d.guidance, nullptr);
     for (std::size_t i = 0; i < L.items.size(); ++i) {

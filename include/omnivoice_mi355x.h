@@ -313,8 +313,8 @@ int ovg_op_linear_noalloc(const void* x, const void* w, float* y, int64_t rows,
  * gemm.cpp:248-262): ovg_op_linear's result through the packed-weight
  * kernel, w packed on the device first (row-major fp16 [out][in] in).
  * `tile_rows` and `tile_cols` 0 take the planned tile; 32, 64, 96 or 128
- * rows by 128 columns, 128 by 256 or 256 by 256 force one (every tile gives
- * the same result bit for bit). */
+ * rows by 128, 64 or 32 columns, 128 by 256 or 256 by 256 force one (every tile
+ * gives the same result bit for bit). */
 int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
                          int64_t in, int64_t out, int accumulate, int64_t tile_rows,
                          int64_t tile_cols, void* stream, char* error, size_t error_len);

@@ -557,11 +557,13 @@ int BandFor(int m, int k, int bm, int splits) {
 // them, are the same whatever else is packed in the batch. Four slices where
 // each keeps at least two K steps (the released o and down: 8 and 12 steps
 // per slice), else three or two.
+// Two splits (K = 2048 and 3072: 16 and 24 K steps each): four halved the
+// K loop of each work-group but doubled the fp32 slices the next add + norm
+// reads back; with two, 10 s 555 -> 570, clone 332 -> 367 and four batched
+// chunks 608 -> 649 unmask steps/s (same box). Small M keeps its
+// parallelism with two-wave tiles (PlanPacked).
 int PartialSplits(int k_steps) {
-  for (const int s : {4, 3, 2})
-    if (k_steps % s == 0 && k_steps / s >= 2)
-      return s;
-  return 1;
+  return k_steps % 2 == 0 && k_steps / 2 >= 2 ? 2 : 1;
 }
 
 GemmPlan PlanGemm(int m, int n, int k, Epilogue epilogue, bool split_small) {

@@ -153,6 +153,7 @@ struct PackedPlan {
   int wb = 1;      // tile width in 128-column units (2: 128 x 256 or 256 x 256)
   int splits = 1;  // K split (partial-slice epilogue only)
   int tiles = 0;   // row tiles x column tiles
+  int nw = 4;      // waves (32-column blocks) of a 32 XB-row tile: 4, 2 or 1
 };
 PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue);
 void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue,

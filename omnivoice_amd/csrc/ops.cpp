@@ -166,11 +166,12 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
     ovg::Require(rows >= 1 && in >= 64 && out >= 1 && FitsInt(rows) &&
                      FitsInt(in) && FitsInt(out),
                  "empty or oversized shape");
-    const bool narrow = tile_cols == 128 && (tile_rows == 32 || tile_rows == 64 ||
-                                             tile_rows == 96 || tile_rows == 128);
+    const bool rows_ok = tile_rows == 32 || tile_rows == 64 || tile_rows == 96 || tile_rows == 128;
+    const bool narrow = (tile_cols == 128 || tile_cols == 64 || tile_cols == 32) && rows_ok;
     const bool wide = tile_cols == 256 && (tile_rows == 128 || tile_rows == 256);
     ovg::Require((tile_rows == 0 && tile_cols == 0) || narrow || wide,
-                 "tile must be 0 x 0 (planned), 32/64/96/128 x 128, 128 x 256 or 256 x 256");
+                 "tile must be 0 x 0 (planned), 32/64/96/128 x 128, 64 or 32, 128 x 256 or "
+                 "256 x 256");
     auto s = static_cast<hipStream_t>(stream);
     const auto epi =
         accumulate ? ovg::Epilogue::kAccumulate : ovg::Epilogue::kStore;
@@ -182,7 +183,8 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
                                            static_cast<int>(in), epi);
     if (tile_rows != 0) {
       plan.xb = static_cast<int>(tile_rows / 32);
-      plan.wb = static_cast<int>(tile_cols / 128);
+      plan.wb = tile_cols == 256 ? 2 : 1;
+      plan.nw = tile_cols == 64 ? 2 : tile_cols == 32 ? 1 : 4;
       plan.tiles = (static_cast<int>(rows) + static_cast<int>(tile_rows) - 1) /
                    static_cast<int>(tile_rows) *
                    ((static_cast<int>(out) + static_cast<int>(tile_cols) - 1) /

@@ -350,10 +350,17 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
   }
 }
 
-template <int XB, Epilogue EPI>
-__global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_m,
-                                                        int k_steps) {
+// NW waves, each owning one packed 32-column block: a (32 XB) x 128 tile
+// with four, (32 XB) x 64 with two, (32 XB) x 32 with one (for small M,
+// where the split-K slices alone leave too few tiles; not for the q/k/v
+// epilogue, which needs a whole 128-column head in one work-group).
+template <int XB, Epilogue EPI, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int tiles_m,
+                                                            int k_steps) {
+  static_assert(NW == 4 || ((NW == 2 || NW == 1) && EPI != Epilogue::kQkvRope),
+                "the q/k/v epilogue needs four waves per 128-column head");
   using S = Packed<XB>;
+  constexpr int XL = 4 * XB / NW;  // X loads (8 rows each) per wave and K step
   extern __shared__ __align__(16) unsigned char lds[];
   // Lane = output row (W as the first MFMA operand) for the epilogues that
   // pair columns inside a lane; lane = output column otherwise, so that the
@@ -373,7 +380,7 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   const int split = rest % p.splits;
   const int tile_n = rest / p.splits;
   // The grid is tiles_m x tiles_n x splits work-groups; nothing past it.
-  if (tile_n * 128 >= p.n)
+  if (tile_n * 32 * NW >= p.n)
     return;
   const int m0 = tile_m * S::kBM;
   const int steps = k_steps / p.splits;  // K steps of this split
@@ -381,16 +388,16 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int block = tile_n * 4 + wave;  // this wave's packed 32-column block
+  const int block = tile_n * NW + wave;  // this wave's packed 32-column block
 
-  // X: wave w brings rows 8 (XB w + i) + lane / 8 of every K step (8 lanes
+  // X: wave w brings rows 8 (XL w + i) + lane / 8 of every K step (8 lanes
   // per 128-byte row), chunk lane % 8, to LDS position Swizzle(row, lane % 8).
   // Rows past M read row M - 1 (their results are never stored).
-  const half8* x_src[XB];
-  int x_dst[XB];
+  const half8* x_src[XL];
+  int x_dst[XL];
 #pragma unroll
-  for (int i = 0; i < XB; ++i) {
-    const int row = 8 * (XB * wave + i) + (lane >> 3);
+  for (int i = 0; i < XL; ++i) {
+    const int row = 8 * (XL * wave + i) + (lane >> 3);
     x_src[i] = reinterpret_cast<const half8*>(
         p.x + static_cast<size_t>(min(m0 + row, p.m - 1)) * p.lda + t0 * 64) + (lane & 7);
     x_dst[i] = row * 128 + Swizzle(row, lane & 7) * 16;
@@ -414,16 +421,16 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
     acc[0][b] = floatx16{};
 
   half8 wf[4][4];       // W of steps t .. t + 3, slot t % 4
-  half8 xs[2][XB];      // X of steps t + 2 and t + 3, slot t % 2
+  half8 xs[2][XL];      // X of steps t + 2 and t + 3, slot t % 2
   half8 fr[2][4][XB];   // fragments of X(t) (slot t % 2) and X(t + 1)
-  auto load_x = [&](half8 (&dst)[XB], int t) {
+  auto load_x = [&](half8 (&dst)[XL], int t) {
 #pragma unroll
-    for (int i = 0; i < XB; ++i)
+    for (int i = 0; i < XL; ++i)
       dst[i] = x_src[i][t * 8];  // 64 halves = 8 half8 per K step
   };
-  auto store_x = [&](const half8 (&src)[XB], int buf) {
+  auto store_x = [&](const half8 (&src)[XL], int buf) {
 #pragma unroll
-    for (int i = 0; i < XB; ++i)
+    for (int i = 0; i < XL; ++i)
       *reinterpret_cast<half8*>(lds + buf * S::kStageBytes + x_dst[i]) = src[i];
   };
   auto read_frag = [&](half8 (&dst)[XB], int buf, int j) {
@@ -448,8 +455,8 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   // two.
   const int last = steps - 1;
   {
-    half8 x0[XB], x1[XB];
-    auto load_step = [&](int s, half8 (&x)[XB]) {
+    half8 x0[XL], x1[XL];
+    auto load_step = [&](int s, half8 (&x)[XL]) {
       const int t = min(s, last);
 #pragma unroll
       for (int j = 0; j < 3; ++j)
@@ -476,7 +483,8 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
   // clocks): after every MFMA one read of X(t + 1)'s fragments from buffer
   // (t + 1) % 4 (written in step t - 1, before the barrier that ended it), so
   // no MFMA waits for LDS; after a substep's last MFMA the reload of its W
-  // slot with W(t + 4); in the last substep, one per row block, the write of
+  // slot with W(t + 4); after the step's last XL MFMAs (the last substep
+  // with four waves, the last two with two), one each, the write of part of
   // X(t + 2) into buffer (t + 2) % 4 (its previous content, X(t - 2), was
   // last read in step t - 3) and the reload of those registers with X(t + 4).
   // The step ends at a barrier that first waits for all of its LDS
@@ -493,8 +501,8 @@ __global__ __launch_bounds__(256) void PackedGemmKernel(GemmParams p, int tiles_
       acc[0][b] = kRowLanes ? Mfma32(wf[ws][j], fr[xo][j][b], acc[0][b])
                             : Mfma32(fr[xo][j][b], wf[ws][j], acc[0][b]);
       __builtin_amdgcn_sched_barrier(0);
-      if (i >= 3 * XB) {
-        const int xi = i - 3 * XB;
+      if (i >= 4 * XB - XL) {
+        const int xi = i - (4 * XB - XL);
         *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) = xs[xo][xi];
         AsmFence();
         xs[xo][xi] = x_src[xi][ahead * 8];
@@ -966,14 +974,29 @@ __global__ void PackWeightsKernel(const T* w, const T* w2, int rows, int k,
   out[o] = v;
 }
 
-template <int XB, Epilogue EPI>
+template <int XB, Epilogue EPI, int NW>
 void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
   const int tiles_m = (p.m + Packed<XB>::kBM - 1) / Packed<XB>::kBM;
-  const int tiles_n = (p.n + 127) / 128;
+  const int tiles_n = (p.n + 32 * NW - 1) / (32 * NW);
   const int groups = tiles_m * tiles_n * p.splits;
   Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
-  Dispatch(PackedGemmKernel<XB, EPI>, dim3(groups), dim3(256), Packed<XB>::kLds, stream, true,
-           true, p, tiles_m, p.k / 64);
+  Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), Packed<XB>::kLds, stream,
+           true, true, p, tiles_m, p.k / 64);
+}
+
+template <int XB, Epilogue EPI>
+void LaunchPackedNarrow(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  if constexpr (EPI != Epilogue::kQkvRope) {
+    if (plan.nw == 2) {
+      LaunchPackedXB<XB, EPI, 2>(p, plan, stream);
+      return;
+    }
+    if (plan.nw == 1) {
+      LaunchPackedXB<XB, EPI, 1>(p, plan, stream);
+      return;
+    }
+  }
+  LaunchPackedXB<XB, EPI, 4>(p, plan, stream);
 }
 
 template <Epilogue EPI>
@@ -1011,10 +1034,10 @@ void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t st
     return;
   }
   switch (plan.xb) {
-    case 1: LaunchPackedXB<1, EPI>(p, plan, stream); break;
-    case 2: LaunchPackedXB<2, EPI>(p, plan, stream); break;
-    case 3: LaunchPackedXB<3, EPI>(p, plan, stream); break;
-    default: LaunchPackedXB<4, EPI>(p, plan, stream); break;
+    case 1: LaunchPackedNarrow<1, EPI>(p, plan, stream); break;
+    case 2: LaunchPackedNarrow<2, EPI>(p, plan, stream); break;
+    case 3: LaunchPackedNarrow<3, EPI>(p, plan, stream); break;
+    default: LaunchPackedNarrow<4, EPI>(p, plan, stream); break;
   }
 }
 
@@ -1071,24 +1094,31 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   // every CU busy a K step takes it 1.45 times as long as the 128 x 256
   // tile's (q/k/v at 3440 rows: 26.5 us of K loop in one round against
   // 36.6 us in 1.7 rounds of the 128 x 256 tile), i.e. 1500 of these clocks.
+  // Two- and one-wave tiles ((32 XB) x 64 or x 32, nw 2 or 1) are priced
+  // the same way: 64 or 32 columns of W per K step, X read by two waves or
+  // one. They come after the four-wave tiles, which win ties.
   struct Shape {
-    int xb, wb;
+    int xb, wb, nw;
   };
   double best = 0.0;
   for (const Shape sh :
-       {Shape{8, 2}, Shape{4, 2}, Shape{4, 1}, Shape{3, 1}, Shape{2, 1}, Shape{1, 1}}) {
+       {Shape{8, 2, 4}, Shape{4, 2, 4}, Shape{4, 1, 4}, Shape{3, 1, 4}, Shape{2, 1, 4},
+        Shape{1, 1, 4}, Shape{4, 1, 2}, Shape{3, 1, 2}, Shape{2, 1, 2}, Shape{1, 1, 2},
+        Shape{2, 1, 1}, Shape{1, 1, 1}}) {
     // The 256 x 256 tile's DMA offsets are 32-bit (X of the generator's
     // GEMMs is [m][k]).
     if (sh.xb == 8 && static_cast<size_t>(m) * k * 2 >= (size_t{1} << 31))
       continue;
-    const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) *
-                      ((n + 128 * sh.wb - 1) / (128 * sh.wb)) * plan.splits;
+    if (sh.nw < 4 && epilogue == Epilogue::kQkvRope)
+      continue;
+    const int cols = 32 * sh.nw * sh.wb;
+    const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) * ((n + cols - 1) / cols) * plan.splits;
     const int full = tiles / kCus, rest = tiles % kCus;
     const double rounds =
         full == 0 ? 1.0
                   : full + (rest == 0 ? 0.0 : std::max(0.5, static_cast<double>(rest) / kCus));
-    const double l2 = (32.0 * sh.xb + 128.0 * sh.wb) * 128.0 / 64.0;
-    const double lds = 5.0 * 32.0 * sh.xb * 128.0 / 128.0;
+    const double l2 = (32.0 * sh.xb + cols) * 128.0 / 64.0;
+    const double lds = (1.0 + sh.nw) * 32.0 * sh.xb * 128.0 / 128.0;
     const double mfma = 4.0 * sh.xb * sh.wb * 32.0;
     const double step = sh.xb == 8 ? 1500.0 : std::max(l2, std::max(lds, mfma));
     const double cost = rounds * (static_cast<double>(steps) * step + 3200.0);
@@ -1096,6 +1126,7 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
       best = cost;
       plan.xb = sh.xb;
       plan.wb = sh.wb;
+      plan.nw = sh.nw;
       plan.tiles = tiles / plan.splits;
     }
   }
@@ -1112,6 +1143,9 @@ void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue
   Require((plan.xb >= 1 && plan.xb <= 4 && (plan.wb == 1 || (plan.wb == 2 && plan.xb == 4))) ||
               (plan.xb == 8 && plan.wb == 2),
           "gemm: tile of 32 to 128 rows x 128 columns, 128 x 256 or 256 x 256");
+  Require(plan.nw == 4 || ((plan.nw == 2 || plan.nw == 1) && plan.wb == 1 && plan.xb <= 4 &&
+                           epilogue != Epilogue::kQkvRope),
+          "gemm: two- and one-wave tiles are 32 to 128 rows x 64 or 32 columns, not for q/k/v");
   switch (epilogue) {
     case Epilogue::kStore:
     case Epilogue::kAccumulate:

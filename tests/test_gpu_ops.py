@@ -144,7 +144,8 @@ def test_packed_linear_matches_float64_at_every_tile(rows, k, n, acc):
         want += y0
     scale = np.sqrt(k) * 0.02
     results = []
-    for tile in ((0, 0), (32, 128), (64, 128), (96, 128), (128, 128), (128, 256), (256, 256)):
+    for tile in ((0, 0), (32, 128), (64, 128), (96, 128), (128, 128), (32, 64), (64, 64),
+                 (96, 64), (128, 64), (32, 32), (64, 32), (128, 256), (256, 256)):
         y = dev(y0)
         ov.op_linear_packed(dev(x), dev(w), y, accumulate=acc, tile_rows=tile[0],
                             tile_cols=tile[1])

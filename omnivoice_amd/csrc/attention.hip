@@ -387,6 +387,14 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // are then formed in place and kept as the fp16 MFMA operand. Scores of up
 // to MAXR tiles per wave live in registers (16 floats per lane, tile and
 // head), so MAXR = 6 covers 768 keys.
+//
+// The phases are bound by different units of the CU: the operand loads by
+// its 64 bytes per clock of load return, the softmax by the quarter-rate
+// exp2, the products by the matrix cores, the merge by LDS. With one head
+// per wave the two heads' waves share a SIMD pairwise and exchange nothing,
+// so they meet per head (HeadSync) rather than at work-group barriers: the
+// head whose operands arrive first runs its softmax and products while the
+// other's loads are still landing.
 constexpr int kExactKeys = 768;
 constexpr int kExactMaxTiles = 6;   // per wave: 4 x 6 x 32 = 768 keys
 
@@ -397,11 +405,47 @@ __device__ __forceinline__ void UnrollEach(F&& f, std::integer_sequence<int, J..
   (f(std::integral_constant<int, J>{}), ...);
 }
 
+// LDS of the exact kernel: the merge's O^T slices (three per wave), and the
+// softmax statistics, maxima then sums. Where the two heads of a group meet
+// separately (one head per wave, two or more key tiles per wave; with one
+// tile the phases are too short to gain from it: 6.00 vs 5.97 us at 70 + 50
+// keys, against 7.07 vs 7.45 at 250 and 8.42 vs 8.90 at 330 + 250), the
+// statistics sit after the merge area, followed by one arrival counter per
+// head and meeting point (HeadSync); otherwise they share its space.
 template <int GROUP>
+constexpr int kExactMerge = 4 * 3 * GROUP * 16 * 64 * 4;
+template <int GROUP>
+constexpr int kExactStats = 2 * GROUP * kRound * 32 * 4;
+constexpr int kMeetings = 3;  // maxima, sums, merge
+template <int GROUP, int HPW, int MAXR>
+constexpr bool kHeadGroups = GROUP / HPW == 2 && MAXR >= 2;
+template <int GROUP, int HPW, int MAXR>
 constexpr int ExactLds() {
-  const int stats = 2 * GROUP * kRound * 32 * 4;  // maxima, then sums
-  const int merge = 4 * 3 * GROUP * 16 * 64 * 4;  // three O^T slices per head
-  return stats > merge ? stats : merge;
+  if constexpr (kHeadGroups<GROUP, HPW, MAXR>)
+    return kExactMerge<GROUP> + kExactStats<GROUP> + GROUP * kMeetings * 4;
+  return kExactStats<GROUP> > kExactMerge<GROUP> ? kExactStats<GROUP> : kExactMerge<GROUP>;
+}
+
+// The four waves of one head meet at an LDS arrival counter (zeroed at the
+// start of the work-group): each waits for its own LDS writes, adds one and
+// waits until all four have. The other head's waves run on, so that one
+// head's softmax and products overlap the other's loads. The wait is
+// bounded: every wave of the work-group reaches every meeting point, so the
+// bound is never reached in a correct run, and it guarantees that no wave
+// can spin forever.
+constexpr int kMeetSpinLimit = 1 << 22;
+__device__ __forceinline__ void HeadSync(unsigned int* counter) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(counter, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int i = 0; i < kMeetSpinLimit; ++i) {
+    const unsigned int arrived =
+        __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(arrived) >= static_cast<unsigned int>(kRound))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" : : : "memory");
 }
 
 template <int GROUP, int MAXR, int HPW>
@@ -469,6 +513,21 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
   load_slot(std::integral_constant<int, 0>{});
   if constexpr (kDepth == 3)
     load_slot(std::integral_constant<int, 1>{});
+  constexpr bool kGroups = kHeadGroups<GROUP, HPW, MAXR>;
+  unsigned int* meet = reinterpret_cast<unsigned int*>(
+      lds + kExactMerge<GROUP> + kExactStats<GROUP>) + head0 * kMeetings;
+  if constexpr (kGroups) {
+    // Zero the counters before anyone arrives; the loads stay in flight.
+    if (threadIdx.x < GROUP * kMeetings)
+      reinterpret_cast<unsigned int*>(lds + kExactMerge<GROUP> + kExactStats<GROUP>)[threadIdx.x] = 0;
+    RingBarrier();
+  }
+  auto meet_head = [&](int point) {
+    if constexpr (kGroups)
+      HeadSync(meet + point);
+    else
+      RingBarrier();
+  };
 
   // Key phase: S^T = K Q^T per tile and head, unscaled; lane holds keys
   // 8 (e / 4) + 4 half_id + e % 4 of its query column. Keys past the
@@ -501,7 +560,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
   // Exact softmax over all keys: per-query maximum of the four quarters,
   // then the sum of e = exp2(c s - c max), c = log2(e) / sqrt(128) (c > 0,
   // so the maximum of the unscaled scores serves), then p = fp16(e / sum).
-  float* smax = reinterpret_cast<float*>(lds);
+  float* smax = reinterpret_cast<float*>(lds + (kGroups ? kExactMerge<GROUP> : 0));
   float* ssum = smax + GROUP * kRound * 32;
   float inverse[HPW];
   {
@@ -519,7 +578,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
       if (half_id == 0)
         smax[((head0 + h) * kRound + quarter) * 32 + col] = m[h];
     }
-    RingBarrier();
+    meet_head(0);
     float sum[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
@@ -538,7 +597,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
       if (half_id == 0)
         ssum[((head0 + h) * kRound + quarter) * 32 + col] = sum[h];
     }
-    RingBarrier();
+    meet_head(1);
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
       const float* hs = ssum + (head0 + h) * kRound * 32 + col;
@@ -586,10 +645,11 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
 
   // The four quarters' outputs are summed as ((0 + 1) + (2 + 3)); wave q
   // finishes dims 32 q .. + 31 of every head, its own part straight from
-  // registers. The statistics are dead once every wave is past the
-  // barrier, so the merge reuses their space.
+  // registers. Where the statistics share the merge's space, they are dead
+  // once every wave is past a barrier.
   floatx4* accs = reinterpret_cast<floatx4*>(lds);
-  RingBarrier();
+  if constexpr (!kGroups)
+    RingBarrier();
 #pragma unroll
   for (int h = 0; h < HPW; ++h)
 #pragma unroll
@@ -603,7 +663,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
             floatx4{o[h][dt][4 * k], o[h][dt][4 * k + 1], o[h][dt][4 * k + 2],
                     o[h][dt][4 * k + 3]};
     }
-  RingBarrier();
+  meet_head(2);
   if (col >= work.q_count)
     return;
 #pragma unroll
@@ -694,18 +754,18 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
     };
     // The kernel instance holds exactly the largest per-wave tile count.
     switch (group * 8 + p.exact_rounds) {
-      case 9: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1>()); break;
-      case 10: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1>()); break;
-      case 11: launch(ExactAttentionKernel<1, 3, 1>, 4, ExactLds<1>()); break;
-      case 12: launch(ExactAttentionKernel<1, 4, 1>, 4, ExactLds<1>()); break;
-      case 13: launch(ExactAttentionKernel<1, 5, 1>, 4, ExactLds<1>()); break;
-      case 14: launch(ExactAttentionKernel<1, 6, 1>, 4, ExactLds<1>()); break;
-      case 17: launch(ExactAttentionKernel<2, 1, 1>, 8, ExactLds<2>()); break;
-      case 18: launch(ExactAttentionKernel<2, 2, 1>, 8, ExactLds<2>()); break;
-      case 19: launch(ExactAttentionKernel<2, 3, 1>, 8, ExactLds<2>()); break;
-      case 20: launch(ExactAttentionKernel<2, 4, 1>, 8, ExactLds<2>()); break;
-      case 21: launch(ExactAttentionKernel<2, 5, 2>, 4, ExactLds<2>()); break;
-      default: launch(ExactAttentionKernel<2, 6, 2>, 4, ExactLds<2>()); break;
+      case 9: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1, 1, 1>()); break;
+      case 10: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1, 1, 2>()); break;
+      case 11: launch(ExactAttentionKernel<1, 3, 1>, 4, ExactLds<1, 1, 3>()); break;
+      case 12: launch(ExactAttentionKernel<1, 4, 1>, 4, ExactLds<1, 1, 4>()); break;
+      case 13: launch(ExactAttentionKernel<1, 5, 1>, 4, ExactLds<1, 1, 5>()); break;
+      case 14: launch(ExactAttentionKernel<1, 6, 1>, 4, ExactLds<1, 1, 6>()); break;
+      case 17: launch(ExactAttentionKernel<2, 1, 1>, 8, ExactLds<2, 1, 1>()); break;
+      case 18: launch(ExactAttentionKernel<2, 2, 1>, 8, ExactLds<2, 1, 2>()); break;
+      case 19: launch(ExactAttentionKernel<2, 3, 1>, 8, ExactLds<2, 1, 3>()); break;
+      case 20: launch(ExactAttentionKernel<2, 4, 1>, 8, ExactLds<2, 1, 4>()); break;
+      case 21: launch(ExactAttentionKernel<2, 5, 2>, 4, ExactLds<2, 2, 5>()); break;
+      default: launch(ExactAttentionKernel<2, 6, 2>, 4, ExactLds<2, 2, 6>()); break;
     }
   }
   if (online) {

@@ -701,6 +701,301 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
   }
 }
 
+
+// --------------------------------------------------- shared-key kernel
+// The exact kernel for two query heads per kv head and at most 512 keys
+// (MAXR <= 4), with the queries and keys fetched once per work-group. The
+// two heads' waves of a quarter use the same key tiles, and every wave of a
+// head the same query tile: loaded straight into registers they cross the
+// CU's load-return path (64 bytes per clock) twice and four times, and at
+// 330 + 250 keys the operand loads (448 KB per CU) take about half of a
+// work-group's time. Here the eight waves copy the two query tiles and every
+// key tile of the sequence into LDS by DMA (a share each, 104 KB at 330
+// keys), meet once, and read their operands from LDS, which returns about
+// four times as many bytes per clock; the value tiles still stream into
+// registers per wave, as in the kernel above. The products, the softmax,
+// the merge and every rounding are the exact kernel's, in the same order,
+// so the two kernels give the same bits.
+//
+// LDS: key tiles [tile][8 KB] and after them the two query tiles, verbatim
+// copies of the operand-order layout; the merge's O^T slices reuse that
+// space once all eight waves are past their key phase (an arrival counter);
+// the statistics and the counters sit after both.
+//
+// The DMAs of a key round (4 tiles, 32 KB) are spread over the eight waves,
+// and a work-group barrier after each round makes its tiles readable to
+// all; the two heads then run on separately from the softmax on, as in the
+// kernel above.
+template <int MAXR>
+constexpr int kSharedKeyBytes = kRound * MAXR * kQBytes;
+template <int MAXR>
+constexpr int kSharedFront = kSharedKeyBytes<MAXR> + 2 * kQBytes > kExactMerge<2>
+                                 ? kSharedKeyBytes<MAXR> + 2 * kQBytes
+                                 : kExactMerge<2>;
+constexpr int kSharedCounters = 2 * kMeetings + 1;  // per head and meeting, keys done
+template <int MAXR>
+constexpr int SharedKeyLds() {
+  return kSharedFront<MAXR> + kExactStats<2> + kSharedCounters * 4;
+}
+
+template <int MAXR>
+__global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams p) {
+  constexpr int GROUP = 2;
+  static_assert(MAXR >= 1 && MAXR <= 4, "shared-key kernel: 1 to 4 key tiles per wave");
+  if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
+    PrefetchWeights(p.prefetch, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
+    return;
+  }
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int g = blockIdx.x % p.kv_heads;
+  const AttentionWork work = p.work[blockIdx.x / p.kv_heads];
+  const int q_begin = __builtin_amdgcn_readfirstlane(work.q_begin);
+  const int seq_begin = __builtin_amdgcn_readfirstlane(work.seq_begin);
+  const int seq_length = __builtin_amdgcn_readfirstlane(work.seq_length);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quarter = wave % kRound;
+  const int head = wave / kRound;  // this wave's query head of the group
+  const int half_id = lane >> 5;
+  const int col = lane & 31;
+  const int tiles = (seq_length + kKTile - 1) / kKTile;
+  const int mine = (tiles - quarter + kRound - 1) / kRound;  // tiles 4 j + quarter < tiles
+  const int block0 = seq_begin >> 4;
+
+  unsigned int* counters =
+      reinterpret_cast<unsigned int*>(lds + kSharedFront<MAXR> + kExactStats<GROUP>);
+  unsigned int* meet = counters + head * kMeetings;
+  unsigned int* keys_done = counters + GROUP * kMeetings;
+
+  // Queries and keys into LDS by wave-wide DMAs of 1 KB, in key rounds:
+  // wave w brings query blocks 2 w and 2 w + 1 (query tile b / 8 of the
+  // group's heads), then in every round r blocks 4 (w % 2) .. + 3 of key
+  // tile 4 r + w / 2 (a tile past the sequence reloads its last tile into a
+  // slot that is never read), so every wave issues the same number of DMAs
+  // and the waits below are compile-time counts. The queries and round 0
+  // land before the first barrier; the later rounds are issued after it
+  // (issued together with round 0 they delay it: 8.4 against 8.26 us at
+  // 330 + 250 keys) and land while the waves compute on the earlier ones.
+  const uint32_t lds0 = LdsAddress(lds);
+  {
+    const unsigned char* q_base = reinterpret_cast<const unsigned char*>(
+        p.qk + static_cast<size_t>(g * GROUP) * p.ld_qk + static_cast<size_t>(q_begin >> 4) * 2048);
+    const size_t q_head_bytes = static_cast<size_t>(p.ld_qk) * 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int b = 2 * wave + i;
+      DmaToLds(q_base + (b >> 3) * q_head_bytes + (b & 7) * 1024, lane * 16,
+               lds0 + kSharedKeyBytes<MAXR> + b * 1024);
+    }
+  }
+  const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
+      p.qk + static_cast<size_t>(p.heads + g) * p.ld_qk + static_cast<size_t>(block0) * 2048);
+  auto dma_round = [&](int r) {
+    const int slot = kRound * r + (wave >> 1);
+    const int t = min(slot, tiles - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = 4 * (wave & 1) + i;
+      DmaToLds(k_base + static_cast<size_t>(t) * kQBytes + blk * 1024, lane * 16,
+               lds0 + slot * kQBytes + blk * 1024);
+    }
+  };
+  dma_round(0);
+  if (threadIdx.x < kSharedCounters)
+    counters[threadIdx.x] = 0;
+  WaitLoads<0>();
+  RingBarrier();
+#pragma unroll
+  for (int r = 1; r < MAXR; ++r)
+    dma_round(r);
+
+  // Operand offsets (bytes) inside a 32-row tile: K step kk of the key and
+  // query operands; value-product operand f = 2 dt + j2 (halves, as above).
+  int k_off[8], v_off[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    k_off[kk] = ((col >> 4) * 2048 + kk * 256 + half_id * 128 + (col & 15) * 8) * 2;
+#pragma unroll
+  for (int f = 0; f < 8; ++f)
+    v_off[f] = (f & 1) * 2048 + (f >> 1) * 512 + lane * 8;
+  const half_t* v_head = p.vt + static_cast<size_t>(g) * kHeadDim * p.ldvt;
+  // Value tile j of this wave into ring slot j % 3, two tiles ahead; tiles
+  // past its last re-read the sequence's last tile and are not used.
+  constexpr int kDepth = 3;
+  half8 buf[kDepth][8];
+  auto load_value = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int t = min(kRound * j + quarter, tiles - 1);
+    const half_t* base = v_head + static_cast<size_t>(block0 + 2 * t) * 2048;
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      buf[j % kDepth][f] = *reinterpret_cast<const half8*>(base + v_off[f]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  half8 qf[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    qf[kk] = *reinterpret_cast<const half8*>(lds + kSharedKeyBytes<MAXR> + head * kQBytes + k_off[kk]);
+
+  // Key phase from LDS: S^T = K Q^T per tile, unscaled, keys past the
+  // sequence -inf (the exact kernel's key phase).
+  floatx16 s[MAXR];
+  auto key_tile = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (j > 0) {
+      // Round j has landed once every wave's own DMAs of it have: only the
+      // later rounds' DMAs may still be in flight.
+      WaitLoads<4 * (MAXR - 1 - j)>();
+      RingBarrier();
+    }
+    if constexpr (j == MAXR - 1) {
+      // The first value tiles once every key tile has landed, so that they
+      // do not queue ahead of the last key round; they have the softmax to
+      // arrive.
+      load_value(std::integral_constant<int, 0>{});
+      if constexpr (MAXR > 1)
+        load_value(std::integral_constant<int, 1>{});
+    }
+    if (j < mine) {
+      const unsigned char* tile = lds + (kRound * j + quarter) * kQBytes;
+      half8 kf[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        kf[kk] = *reinterpret_cast<const half8*>(tile + k_off[kk]);
+      const int valid_keys = seq_length - (kRound * j + quarter) * kKTile;
+      floatx16 acc = floatx16{};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        acc = Mfma32(kf[kk], qf[kk], acc);
+      s[j] = acc;
+      if (valid_keys < kKTile)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = 8 * (e / 4) + 4 * half_id + (e & 3);
+          s[j][e] = key < valid_keys ? s[j][e] : -__builtin_inff();
+        }
+    }
+  };
+  UnrollEach(key_tile, std::make_integer_sequence<int, MAXR>{});
+  // This wave's last reads of the query and key tiles are done.
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  if (lane == 0)
+    __hip_atomic_fetch_add(keys_done, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+
+  // Exact softmax (the exact kernel's, per head).
+  float* smax = reinterpret_cast<float*>(lds + kSharedFront<MAXR>);
+  float* ssum = smax + GROUP * kRound * 32;
+  float inverse;
+  {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < MAXR; ++j)
+      if (j < mine)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          m = fmaxf(m, s[j][e]);
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (half_id == 0)
+      smax[(head * kRound + quarter) * 32 + col] = m;
+    HeadSync(meet + 0);
+    const float* hm = smax + head * kRound * 32 + col;
+    const float shift = -(fmaxf(fmaxf(hm[0], hm[32]), fmaxf(hm[64], hm[96])) * p.scale_log2);
+    float sum = 0.0F;
+#pragma unroll
+    for (int j = 0; j < MAXR; ++j)
+      if (j < mine)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          s[j][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][e], p.scale_log2, shift));
+          sum += s[j][e];
+        }
+    sum += __shfl_xor(sum, 32);
+    if (half_id == 0)
+      ssum[(head * kRound + quarter) * 32 + col] = sum;
+    HeadSync(meet + 1);
+    const float* hs = ssum + head * kRound * 32 + col;
+    inverse = 1.0F / ((hs[0] + hs[32]) + (hs[64] + hs[96]));
+  }
+  half8 pf[MAXR][2];
+#pragma unroll
+  for (int j = 0; j < MAXR; ++j)
+    if (j < mine)
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pf[j][j2][e] = static_cast<half_t>(s[j][8 * j2 + e] * inverse);
+
+  // Value phase: O^T = V^T P^T over this quarter's tiles.
+  floatx16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    o[dt] = floatx16{};
+  auto value_tile = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (j + kDepth - 1 < MAXR)
+      load_value(std::integral_constant<int, j + kDepth - 1>{});
+    if (j < mine) {
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          o[dt] = Mfma32(buf[j % kDepth][2 * dt + j2], pf[j][j2], o[dt]);
+    }
+  };
+  UnrollEach(value_tile, std::make_integer_sequence<int, MAXR>{});
+
+  // Merge (the exact kernel's), once no wave reads the key tiles any more.
+  for (int i = 0; i < kMeetSpinLimit; ++i) {
+    const unsigned int done =
+        __hip_atomic_load(keys_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(done) >= static_cast<unsigned int>(GROUP * kRound))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" : : : "memory");
+  floatx4* accs = reinterpret_cast<floatx4*>(lds);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    if (dt == quarter)
+      continue;
+    const int part = dt < quarter ? dt : dt - 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      accs[(((quarter * 3 + part) * GROUP + head) * 4 + k) * 64 + lane] =
+          floatx4{o[dt][4 * k], o[dt][4 * k + 1], o[dt][4 * k + 2], o[dt][4 * k + 3]};
+  }
+  HeadSync(meet + 2);
+  if (col >= work.q_count)
+    return;
+  const floatx16 own = quarter == 0 ? o[0] : quarter == 1 ? o[1] : quarter == 2 ? o[2] : o[3];
+  auto load = [&](int q) {
+    if (q == quarter)
+      return own;
+    const int part = quarter < q ? quarter : quarter - 1;
+    floatx16 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const floatx4 x = accs[(((q * 3 + part) * GROUP + head) * 4 + k) * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[4 * k + i] = x[i];
+    }
+    return v;
+  };
+  const floatx16 result = (load(0) + load(1)) + (load(2) + load(3));
+  half_t* out = p.out + static_cast<size_t>(q_begin + col) * p.heads * kHeadDim +
+                (g * GROUP + head) * kHeadDim + quarter * 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    half4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = static_cast<half_t>(result[4 * q + e]);
+    *reinterpret_cast<half4*>(out + 8 * q + 4 * half_id) = v;
+  }
+}
+
 }  // namespace
 
 void PlanAttentionWork(std::vector<AttentionWork>& work, int* exact_count,
@@ -753,6 +1048,14 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
       Dispatch(kernel, grid, dim3(64 * waves), lds_bytes, stream, true, !online, e);
     };
     // The kernel instance holds exactly the largest per-wave tile count.
+    if (group == 2 && p.exact_rounds <= 4) {
+      switch (p.exact_rounds) {
+        case 1: launch(SharedKeyAttentionKernel<1>, 8, SharedKeyLds<1>()); break;
+        case 2: launch(SharedKeyAttentionKernel<2>, 8, SharedKeyLds<2>()); break;
+        case 3: launch(SharedKeyAttentionKernel<3>, 8, SharedKeyLds<3>()); break;
+        default: launch(SharedKeyAttentionKernel<4>, 8, SharedKeyLds<4>()); break;
+      }
+    } else {
     switch (group * 8 + p.exact_rounds) {
       case 9: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1, 1, 1>()); break;
       case 10: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1, 1, 2>()); break;
@@ -766,6 +1069,7 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
       case 20: launch(ExactAttentionKernel<2, 4, 1>, 8, ExactLds<2, 1, 4>()); break;
       case 21: launch(ExactAttentionKernel<2, 5, 2>, 4, ExactLds<2, 2, 5>()); break;
       default: launch(ExactAttentionKernel<2, 6, 2>, 4, ExactLds<2, 2, 6>()); break;
+    }
     }
   }
   if (online) {

@@ -255,23 +255,25 @@ def test_attention_head_groups_and_limits(heads, kv, seqs):
         assert err < 1.5e-2 and rel < 3e-3, (length, err, rel)
 
 
-def test_attention_batch_invariant():
+@pytest.mark.parametrize("length", [100, 300, 500])
+def test_attention_batch_invariant(length):
     """A sequence's attention output does not depend on what else is packed
-    beside it: alone (one round of keys held in registers) and packed after
-    a 700-key sequence (the kernel instance that holds six rounds) or a
-    1500-key one (the online-softmax kernel for that one) it is bit for bit
-    the same."""
-    rng = np.random.default_rng(77)
+    beside it: alone (one, three or four rounds of keys, taken by the kernel
+    that shares the keys through LDS) and packed after a 700-key sequence
+    (the register-fed kernel instance that holds six rounds) or a 1500-key
+    one (the online-softmax kernel for that one) it is bit for bit the
+    same."""
+    rng = np.random.default_rng(77 + length)
     heads, kv = 16, 8
     width = (heads + 2 * kv) * 128
-    seq = (rng.standard_normal((100, width)) * 1.5).astype(np.float16)
+    seq = (rng.standard_normal((length, width)) * 1.5).astype(np.float16)
     outs = []
     for before in (0, 700, 1500):
         start = (before + 15) // 16 * 16
-        rows = start + 100
+        rows = start + length
         qkv = (rng.standard_normal((rows, width)) * 1.5).astype(np.float16)
         qkv[start:] = seq
-        seqs = [(start, 100)] if before == 0 else [(0, before), (start, 100)]
+        seqs = [(start, length)] if before == 0 else [(0, before), (start, length)]
         out = torch.zeros((rows, heads * 128), dtype=torch.float16, device="cuda")
         ov.op_attention(dev(qkv), out, heads, kv, seqs)
         outs.append(host(out)[start:])

@@ -82,6 +82,16 @@ constexpr int kWideLds = Packed<4>::kLds > kWideSums + 2 * kHeadStage<4>
                              : kWideSums + 2 * kHeadStage<4>;
 static_assert(512 * 4 + kHeadStage<4> <= Packed<4>::kLds, "narrow q/k staging");
 
+// The narrow tile's q/k/v instances stage the tile's rotary rows in LDS
+// after the ring: 32 XB rows of 64 (cos, sin) pairs (512 bytes), 16-byte
+// chunk c of row r at position c ^ (r % 32), so that the epilogue's reads
+// (32 lanes, 32 rows, one chunk each) are free of bank conflicts.
+constexpr int kRopeRowBytes = 64 * 8;
+template <int XB, Epilogue EPI>
+constexpr int NarrowLds() {
+  return Packed<XB>::kLds + (EPI == Epilogue::kQkvRope ? 32 * XB * kRopeRowBytes : 0);
+}
+
 // 16-byte chunk c of LDS row r sits at position c ^ (r & 7) ^ ((r >> 3) & 1);
 // its own inverse.
 __device__ __forceinline__ int Swizzle(int row, int chunk) {
@@ -123,7 +133,8 @@ __host__ __device__ __forceinline__ int QkvHead(int slot, int total, int group) 
 template <int XB, int WB, Epilogue EPI>
 __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc)[WB][XB],
                                              int m0, int split, int block0, int wave,
-                                             int lane, unsigned char* lds, int stage) {
+                                             int lane, unsigned char* lds, int stage,
+                                             int rope_stage = -1) {
   constexpr int kBM = 32 * XB;
   const int h = lane >> 5;
   const int col = lane & 31;
@@ -192,9 +203,12 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
     // block ahead into one of two register sets; the first block's before
     // the sums, so that their latency overlaps the sums and the barrier
     // rather than stalling once per block. Rows past M read row M - 1.
+    // With `rope_stage` >= 0 the tile's rotary rows are already in LDS
+    // there (one block per wave): they are read after the barrier.
+    const bool staged = rope_stage >= 0;
     float2 rot[2][XB][8];
     float wt[2][16];  // w_lo[g][i] at 4 g + i, w_hi at 8 + 4 g + i
-    auto load_rope = [&](int buf, int wb) {
+    auto load_weights = [&](int buf, int wb) {
       const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
 #pragma unroll
       for (int g = 0; g < 2; ++g)
@@ -203,19 +217,43 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           wt[buf][4 * g + i] = weight[c_base + 8 * g + i];
           wt[buf][8 + 4 * g + i] = weight[64 + c_base + 8 * g + i];
         }
+    };
+    auto load_rot = [&](int buf, int wb) {
+      const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
 #pragma unroll
       for (int b = 0; b < XB; ++b) {
-        const int m = min(m0 + 32 * b + col, p.m - 1);
-        const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
+        if (staged) {
+          // Pairs c_base + 8 g .. + 3 are chunks (c_base + 8 g) / 2 and + 1.
+          const unsigned char* row = lds + rope_stage + (32 * b + col) * kRopeRowBytes;
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+          for (int g = 0; g < 2; ++g)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            rot[buf][b][4 * g + i] = cs[8 * g + i];
+            for (int k = 0; k < 2; ++k) {
+              const int chunk = (c_base + 8 * g) / 2 + k;
+              const float4 v = *reinterpret_cast<const float4*>(row + ((chunk ^ col) << 4));
+              rot[buf][b][4 * g + 2 * k] = make_float2(v.x, v.y);
+              rot[buf][b][4 * g + 2 * k + 1] = make_float2(v.z, v.w);
+            }
+        } else {
+          const int m = min(m0 + 32 * b + col, p.m - 1);
+          const float2* cs = p.rope + static_cast<size_t>(m) * 64 + c_base;
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              rot[buf][b][4 * g + i] = cs[8 * g + i];
+        }
       }
     };
-    if (qk)
-      load_rope(0, 0);
+    auto load_rope = [&](int buf, int wb) {
+      load_weights(buf, wb);
+      load_rot(buf, wb);
+    };
+    if (qk) {
+      load_weights(0, 0);
+      if (!staged)
+        load_rot(0, 0);
+    }
     // Sum of squares of each block's 32 columns of a row, then over the
     // head's four blocks in the fixed order (0 + 1) + (2 + 3): a wave adds
     // its own pair when it holds two blocks, or all four when it holds the
@@ -240,7 +278,11 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
           sums[wave * kBM + 32 * b + col] = WB == 2 ? part[0][b] + part[WB - 1][b] : part[0][b];
       }
     }
+    if (staged)
+      WaitLoads<0>();  // this wave's share of the staged rotary rows
     Barrier();  // LDS only: the rotary loads stay in flight
+    if (qk && staged)
+      load_rot(0, 0);
     // q/k heads: normalised and rotated values go to this head's LDS
     // staging rows (32 XB rows of 256 bytes at `stage`, 16-byte chunk c of
     // row r at position c ^ (r % 16)), from which the waves that share the
@@ -354,7 +396,7 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
 // with four, (32 XB) x 64 with two, (32 XB) x 32 with one (for small M,
 // where the split-K slices alone leave too few tiles; not for the q/k/v
 // epilogue, which needs a whole 128-column head in one work-group).
-template <int XB, Epilogue EPI, int NW = 4>
+template <int XB, Epilogue EPI, int NW = 4, bool ANY_K = false>
 __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int tiles_m,
                                                             int k_steps) {
   static_assert(NW == 4 || ((NW == 2 || NW == 1) && EPI != Epilogue::kQkvRope),
@@ -454,6 +496,30 @@ __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int ti
   // made two steps in four wait for loads issued one step earlier instead of
   // two.
   const int last = steps - 1;
+  // q/k tiles stage their 32 XB rotary rows (512 bytes each) in LDS after
+  // the ring: XB 1 KB DMAs per wave in each of the last four K steps, which
+  // issue no operand loads (nothing in the loop waits for them, and they
+  // take none of the operand stream's bandwidth: issued in the earlier
+  // steps they slowed the loop by as much as they saved), so that the
+  // epilogue reads LDS instead of a row-strided table (issuing those loads
+  // after the loop took ~1.5 K clocks at 580 rows).
+  // Block i of wave w holds tile rows 2 (4 XB w + i) and + 1; lane l writes
+  // chunk (l % 32) ^ (row % 32) of row + l / 32. Rows past M read row M - 1.
+  bool stage_rope = false;
+  if constexpr (EPI == Epilogue::kQkvRope && !ANY_K) {
+    const int slot = QkvHead(tile_n, p.heads + 2 * p.kv_heads, p.heads / p.kv_heads);
+    stage_rope = slot >= 0 && slot < p.heads + p.kv_heads;
+  }
+  const unsigned char* rope_base =
+      reinterpret_cast<const unsigned char*>(p.rope + static_cast<size_t>(m0) * 64);
+  const uint32_t rope_lds = LdsAddress(lds) + S::kLds + wave * 4 * XB * 1024;
+  auto stage_rope_block = [&](int i) {
+    const int row = 2 * (4 * XB * wave + i) + (lane >> 5);
+    const int chunk = (lane & 31) ^ (row & 31);
+    const uint32_t off = static_cast<uint32_t>((min(m0 + row, p.m - 1) - m0) * kRopeRowBytes +
+                                               chunk * 16);
+    DmaToLds(rope_base, off, rope_lds + i * 1024);
+  };
   {
     half8 x0[XL], x1[XL];
     auto load_step = [&](int s, half8 (&x)[XL]) {
@@ -491,9 +557,20 @@ __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int ti
   // operations, after which X(t + 2) is readable. (Writing X(t + 2) in the
   // first substep instead measured 1-3 % slower at 580 rows; letting the
   // fragment reads run on across the barrier measured no faster.)
-  auto step = [&](int t, auto slot) {
+  //
+  // RELOAD, WRITE and READ (compile-time) switch off the step's global
+  // reloads, its write of X(t + 2) and its reads of X(t + 1)'s fragments
+  // where those steps are past the last: the last four steps of a K range
+  // that is a multiple of four steps issue no loads, so that the epilogue's
+  // loads and stores do not queue behind 28 KB per wave of clamped reloads
+  // that nothing uses (at 580 x 4096 x 1024 they took ~2 K clocks to drain
+  // before the q/k/v epilogue's first loads could issue).
+  auto step = [&](int t, auto slot, auto reload, auto write, auto read) {
     constexpr int ws = decltype(slot)::value;  // t % 4
     constexpr int xo = ws & 1;                 // t % 2
+    constexpr bool kReload = decltype(reload)::value;
+    constexpr bool kWrite = decltype(write)::value;
+    constexpr bool kRead = decltype(read)::value;
     const int ahead = min(t + 4, last);
 #pragma unroll
     for (int i = 0; i < 4 * XB; ++i) {
@@ -503,15 +580,28 @@ __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int ti
       __builtin_amdgcn_sched_barrier(0);
       if (i >= 4 * XB - XL) {
         const int xi = i - (4 * XB - XL);
-        *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) = xs[xo][xi];
-        AsmFence();
-        xs[xo][xi] = x_src[xi][ahead * 8];
+        if constexpr (kWrite) {
+          *reinterpret_cast<half8*>(lds + ((ws + 2) & 3) * S::kStageBytes + x_dst[xi]) =
+              xs[xo][xi];
+          AsmFence();
+        }
+        if constexpr (kReload)
+          xs[xo][xi] = x_src[xi][ahead * 8];
       }
-      fr[1 - xo][i / XB][i % XB] = *reinterpret_cast<const half8*>(
-          lds + ((ws + 1) & 3) * S::kStageBytes + x_read[i % XB][i / XB]);
-      if (b == XB - 1)
-        wf[ws][j] = w_src[(ahead * 4 + j) * 64];
+      if constexpr (kRead)
+        fr[1 - xo][i / XB][i % XB] = *reinterpret_cast<const half8*>(
+            lds + ((ws + 1) & 3) * S::kStageBytes + x_read[i % XB][i / XB]);
+      if constexpr (kReload)
+        if (b == XB - 1)
+          wf[ws][j] = w_src[(ahead * 4 + j) * 64];
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EPI == Epilogue::kQkvRope && !kReload) {
+      // The last four steps (slot = step - (steps - 4)): XB blocks each.
+      if (stage_rope)
+#pragma unroll
+        for (int i = 0; i < XB; ++i)
+          stage_rope_block(ws * XB + i);
     }
     Barrier();
   };
@@ -519,24 +609,43 @@ __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int ti
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  const int whole = steps & ~3;
-  for (int t = 0; t < whole; t += 4) {
-    step(t, I0{});
-    step(t + 1, I1{});
-    step(t + 2, I2{});
-    step(t + 3, I3{});
+  using On = std::true_type;
+  using Off = std::false_type;
+  if constexpr (!ANY_K) {
+    // K range per split a multiple of four steps (every shape of the model).
+    const int body = steps - 4;
+    for (int t = 0; t < body; t += 4) {
+      step(t, I0{}, On{}, On{}, On{});
+      step(t + 1, I1{}, On{}, On{}, On{});
+      step(t + 2, I2{}, On{}, On{}, On{});
+      step(t + 3, I3{}, On{}, On{}, On{});
+    }
+    step(body, I0{}, Off{}, On{}, On{});
+    step(body + 1, I1{}, Off{}, On{}, On{});
+    step(body + 2, I2{}, Off{}, Off{}, On{});
+    step(body + 3, I3{}, Off{}, Off{}, Off{});
+  } else {
+    // Any K range (a separate instance, so that the loop above keeps its
+    // registers): every step reloads, clamped to the last step, and the
+    // last steps % 4 run after the groups of four.
+    const int whole = steps & ~3;
+    for (int t = 0; t < whole; t += 4) {
+      step(t, I0{}, On{}, On{}, On{});
+      step(t + 1, I1{}, On{}, On{}, On{});
+      step(t + 2, I2{}, On{}, On{}, On{});
+      step(t + 3, I3{}, On{}, On{}, On{});
+    }
+    if (whole < steps)
+      step(whole, I0{}, On{}, On{}, On{});
+    if (whole + 1 < steps)
+      step(whole + 1, I1{}, On{}, On{}, On{});
+    if (whole + 2 < steps)
+      step(whole + 2, I2{}, On{}, On{}, On{});
   }
-  // The last steps % 4 steps (only shapes whose K range per split is not a
-  // multiple of 256).
-  if (whole < steps)
-    step(whole, I0{});
-  if (whole + 1 < steps)
-    step(whole + 1, I1{});
-  if (whole + 2 < steps)
-    step(whole + 2, I2{});
 
   // q/k staging after the LDS sums ([4][32 XB] floats).
-  WaveEpilogue<XB, 1, EPI>(p, acc, m0, split, block, wave, lane, lds, 512 * XB);
+  WaveEpilogue<XB, 1, EPI>(p, acc, m0, split, block, wave, lane, lds, 512 * XB,
+                           stage_rope ? S::kLds : -1);
 }
 
 // The wide tile for large M: 128 x 256, each wave owning two packed blocks
@@ -980,8 +1089,14 @@ void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t str
   const int tiles_n = (p.n + 32 * NW - 1) / (32 * NW);
   const int groups = tiles_m * tiles_n * p.splits;
   Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
-  Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), Packed<XB>::kLds, stream,
-           true, true, p, tiles_m, p.k / 64);
+  if ((p.k / 64 / p.splits) % 4 == 0) {
+    Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), NarrowLds<XB, EPI>(),
+             stream, true, true, p, tiles_m, p.k / 64);
+    return;
+  }
+  // K ranges that are not a multiple of 256 per split (small models).
+  Dispatch(PackedGemmKernel<XB, EPI, NW, true>, dim3(groups), dim3(64 * NW),
+           NarrowLds<XB, EPI>(), stream, true, true, p, tiles_m, p.k / 64);
 }
 
 template <int XB, Epilogue EPI>

@@ -502,13 +502,15 @@ __global__ __launch_bounds__(64 * NW) void PackedGemmKernel(GemmParams p, int ti
   // take none of the operand stream's bandwidth: issued in the earlier
   // steps they slowed the loop by as much as they saved), so that the
   // epilogue reads LDS instead of a row-strided table (issuing those loads
-  // after the loop took ~1.5 K clocks at 580 rows).
+  // after the loop took ~1.5 K clocks at 580 rows). Only where the grid is
+  // one round of work-groups: the 48 KB more LDS per work-group would keep
+  // a second one off a CU (1055 rows: q/k/v 19.2 -> 21.2 us).
   // Block i of wave w holds tile rows 2 (4 XB w + i) and + 1; lane l writes
   // chunk (l % 32) ^ (row % 32) of row + l / 32. Rows past M read row M - 1.
   bool stage_rope = false;
   if constexpr (EPI == Epilogue::kQkvRope && !ANY_K) {
     const int slot = QkvHead(tile_n, p.heads + 2 * p.kv_heads, p.heads / p.kv_heads);
-    stage_rope = slot >= 0 && slot < p.heads + p.kv_heads;
+    stage_rope = groups <= kCus && slot >= 0 && slot < p.heads + p.kv_heads;
   }
   const unsigned char* rope_base =
       reinterpret_cast<const unsigned char*>(p.rope + static_cast<size_t>(m0) * 64);
@@ -1090,13 +1092,16 @@ void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t str
   const int groups = tiles_m * tiles_n * p.splits;
   Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
   if ((p.k / 64 / p.splits) % 4 == 0) {
-    Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), NarrowLds<XB, EPI>(),
-             stream, true, true, p, tiles_m, p.k / 64);
+    // The q/k/v tile stages its rotary rows when the grid is one round
+    // (the kernel makes the same test on its grid size).
+    const int lds = groups <= kCus ? NarrowLds<XB, EPI>() : Packed<XB>::kLds;
+    Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), lds, stream, true,
+             true, p, tiles_m, p.k / 64);
     return;
   }
   // K ranges that are not a multiple of 256 per split (small models).
-  Dispatch(PackedGemmKernel<XB, EPI, NW, true>, dim3(groups), dim3(64 * NW),
-           NarrowLds<XB, EPI>(), stream, true, true, p, tiles_m, p.k / 64);
+  Dispatch(PackedGemmKernel<XB, EPI, NW, true>, dim3(groups), dim3(64 * NW), Packed<XB>::kLds,
+           stream, true, true, p, tiles_m, p.k / 64);
 }
 
 template <int XB, Epilogue EPI>

@@ -856,6 +856,226 @@ __device__ __forceinline__ int Swizzle32(int row, int q) {
   return q ^ ((row >> 1) & 3) ^ ((row >> 3) & 1);
 }
 
+// The q/k/v epilogue of the 256 x 256 tile, where a wave holds one whole
+// head (its four packed blocks) for 128 rows. The rotary rows of its 128
+// rows are 64 KB, which the general epilogue loads block by block from the
+// row-strided table (16 loads per lane and block, each touching 32 rows
+// 512 bytes apart): at 3440 rows that took ~15 K of a launch's ~65 K clocks
+// (41.6 against 37.5 us with constants in their place). Here the four waves
+// copy the tile's 256 rotary rows (128 KB) into LDS by DMA once the K loop
+// has freed the ring (chunk c of row r at position c ^ (r % 32), so the
+// reads are conflict-free), and each wave stages and stores its head one
+// 32-column block at a time (8 KB of LDS per wave instead of 32 KB, which
+// leaves the room). Every value is computed and rounded as in WaveEpilogue.
+constexpr int kBigStage = 8192;                    // per wave, one block
+constexpr int kBigRope = 4 * kBigStage;            // 256 rows x 512 bytes after it
+constexpr int kBigQkvLds = kBigRope + 256 * kRopeRowBytes;
+static_assert(kBigQkvLds >= kBigLds && kBigQkvLds <= 160 * 1024, "q/k/v tile LDS");
+
+__device__ __forceinline__ void BigQkvEpilogue(const GemmParams& p, floatx16 (&acc)[4][4],
+                                               int tile_m0, int wr, int block0, int wave,
+                                               int lane, unsigned char* lds) {
+  constexpr int XB = 4, WB = 4, kBM = 128;
+  const int h = lane >> 5;
+  const int col = lane & 31;
+  const int m0 = tile_m0 + 128 * wr;
+  const int total = p.heads + 2 * p.kv_heads;
+  const int slot = QkvHead(block0 / 4, total, p.heads / p.kv_heads);
+  const bool live = block0 * 32 < p.n && slot >= 0;
+  const bool qk = live && slot < p.heads + p.kv_heads;
+  const float* weight = slot < p.heads ? p.q_norm : p.k_norm;
+  // Rotary rows of the tile in four pieces, piece k the pairs 16 k .. + 15
+  // (16-byte chunks 8 k .. + 7) of all 256 rows, 32 KB at kBigRope + 32 KB
+  // k: row r's 128 bytes at 128 r, chunk c at position c ^ ((r / 2) % 8)
+  // (conflict-free reads). DMA block i of a piece covers rows 8 i .. + 7,
+  // wave w taking blocks 8 w .. 8 w + 7 of every piece, pieces in order, so
+  // that piece k has landed everywhere once each wave has waited for its
+  // own DMAs of pieces 0 .. k and the work-group has met. Rows past M read
+  // row M - 1.
+  const unsigned char* rope_base =
+      reinterpret_cast<const unsigned char*>(p.rope + static_cast<size_t>(tile_m0) * 64);
+  const uint32_t rope_dst = LdsAddress(lds) + kBigRope + wave * 8 * 1024;
+  auto dma_piece = [&](int k) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 8 * (8 * wave + i) + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      const uint32_t off = static_cast<uint32_t>(
+          (min(tile_m0 + row, p.m - 1) - tile_m0) * kRopeRowBytes + (8 * k + chunk) * 16);
+      DmaToLds(rope_base, off, rope_dst + k * 32768 + i * 1024);
+    }
+  };
+  // Piece 0, then the norm weights of all four blocks, which are waited for
+  // (with piece 0, needed first anyway) before pieces 1 .. 3 are issued: the
+  // compiler's wait for a load of its own would otherwise also wait for the
+  // DMAs issued after it.
+  dma_piece(0);
+  float wt[WB][16];  // w_lo[g][i] at 4 g + i, w_hi at 8 + 4 g + i
+  if (qk) {
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb) {
+      const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wt[wb][4 * g + i] = weight[c_base + 8 * g + i];
+          wt[wb][8 + 4 * g + i] = weight[64 + c_base + 8 * g + i];
+        }
+    }
+  }
+  float scale[XB];
+  if (qk) {
+    // The head's sum of squares per row: each block's 32 columns, then the
+    // four blocks as (0 + 1) + (2 + 3).
+    float part[WB][XB];
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb)
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        float s = acc[wb][b][0] * acc[wb][b][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r)
+          s = __builtin_fmaf(acc[wb][b][r], acc[wb][b][r], s);
+        part[wb][b] = s + __shfl_xor(s, 32);
+      }
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      const float t = (part[0][b] + part[1][b]) + (part[2][b] + part[3][b]);
+      scale[b] = rsqrtf(__builtin_fmaf(t, 1.0F / 128.0F, p.eps));
+    }
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        asm volatile("" : : "v"(wt[wb][i]));
+  }
+  WaitLoads<0>();
+  dma_piece(1);
+  dma_piece(2);
+  dma_piece(3);
+  // Waits until piece k has landed in the whole work-group (piece 0: at
+  // the wait above). The count assumes no later memory instruction; the
+  // blocks' stores, issued after the DMAs, count too, so the wait can only
+  // be longer than needed, never shorter.
+  auto piece_ready = [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    WaitLoads<8 * (3 - k)>();
+    __builtin_amdgcn_s_barrier();
+    AsmFence();
+  };
+  unsigned char* stage = lds + wave * kBigStage;
+  // Block wb uses piece (block0 + wb) % 4 = wb (block0 is a multiple of 4);
+  // every wave meets at all four points, whatever its head.
+  if (qk) {
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb) {
+      if (wb == 0) piece_ready(std::integral_constant<int, 0>{});
+      if (wb == 1) piece_ready(std::integral_constant<int, 1>{});
+      if (wb == 2) piece_ready(std::integral_constant<int, 2>{});
+      if (wb == 3) piece_ready(std::integral_constant<int, 3>{});
+      const int c_base = 16 * ((block0 + wb) & 3) + 4 * h;
+      const int chunk0 = 2 * ((block0 + wb) & 3);
+      // Rotated, normalised q/k of this block: row r_local = 32 b + col,
+      // position g (lo, chunk chunk0 + g) or 2 + g (hi, chunk chunk0 + 8 + g)
+      // of its 64-byte staging row, swizzled by (r / 4) % 4, half h.
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int rr = 128 * wr + 32 * b + col;  // tile row
+        const unsigned char* rope_row = lds + kBigRope + wb * 32768 + rr * 128;
+        float2 rot[8];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int chunk = (c_base + 8 * g) / 2 + k - 8 * wb;  // within the piece
+            const float4 v =
+                *reinterpret_cast<const float4*>(rope_row + ((chunk ^ ((rr >> 1) & 7)) << 4));
+            rot[4 * g + 2 * k] = make_float2(v.x, v.y);
+            rot[4 * g + 2 * k + 1] = make_float2(v.z, v.w);
+          }
+        const int r_local = 32 * b + col;
+        unsigned char* row = stage + r_local * 64 + 8 * h;
+        const int swz = (r_local >> 2) & 3;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          half4 lo, hi;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float2 cs = rot[4 * g + i];
+            const float a = wt[wb][4 * g + i] * (acc[wb][b][4 * g + i] * scale[b]);
+            const float bb = wt[wb][8 + 4 * g + i] * (acc[wb][b][4 * g + 8 + i] * scale[b]);
+            lo[i] = static_cast<half_t>(__builtin_fmaf(a, cs.x, -(bb * cs.y)));
+            hi[i] = static_cast<half_t>(__builtin_fmaf(bb, cs.x, a * cs.y));
+          }
+          *reinterpret_cast<half4*>(row + ((g ^ swz) << 4)) = lo;
+          *reinterpret_cast<half4*>(row + (((2 + g) ^ swz) << 4)) = hi;
+        }
+      }
+      AsmFence();
+      // Copy-out in the attention's fragment order (QkIndex): 16 lanes store
+      // one chunk of 16 consecutive rows, a 256-byte run.
+#pragma unroll
+      for (int pass = 0; pass < 8; ++pass) {
+        const int e = pass * 64 + lane;
+        const int r = (e & 15) + 16 * (e >> 6);
+        const int pos = (e >> 4) & 3;
+        const int q = pos < 2 ? chunk0 + pos : chunk0 + 8 + (pos - 2);
+        const half8 v = *reinterpret_cast<const half8*>(
+            stage + r * 64 + ((pos ^ ((r >> 2) & 3)) << 4));
+        if (m0 + r < p.m)
+          *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m0 + r, 8 * q, p.ldq)) = v;
+      }
+      AsmFence();
+    }
+  } else if (live) {
+    // Value head: per block, V^T of its 32 dims (d_local = d % 16 + 16 (d /
+    // 64)) x 128 rows in VtColumn order, then 16-byte chunks of 8 keys
+    // (VtIndex).
+    const int gv = slot - p.heads - p.kv_heads;
+#pragma unroll
+    for (int wb = 0; wb < WB; ++wb) {
+      if (wb == 0) piece_ready(std::integral_constant<int, 0>{});
+      if (wb == 1) piece_ready(std::integral_constant<int, 1>{});
+      if (wb == 2) piece_ready(std::integral_constant<int, 2>{});
+      if (wb == 3) piece_ready(std::integral_constant<int, 3>{});
+      const int blk = (block0 + wb) & 3;
+      const int c_base = 16 * blk + 4 * h;
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int r_local = VtColumn(32 * b + col);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int d = c_base + 8 * ((r >> 2) & 1) + (r & 3) + 64 * (r >> 3);
+          const int d_local = (d & 15) + 16 * (d >> 6);
+          *reinterpret_cast<half_t*>(stage + (d_local * kBM + r_local) * 2) =
+              static_cast<half_t>(acc[wb][b][r]);
+        }
+      }
+      AsmFence();
+#pragma unroll
+      for (int pass = 0; pass < 8; ++pass) {
+        const int e = pass * 64 + lane;
+        const int d_local = e & 31, half = (e >> 5) & 1, b16 = e >> 6;
+        const int d = (d_local & 15) + 16 * blk + 64 * (d_local >> 4);
+        const half8 v = *reinterpret_cast<const half8*>(
+            stage + (d_local * kBM + 16 * b16 + 8 * half) * 2);
+        if (m0 + 16 * b16 < p.m)
+          *reinterpret_cast<half8*>(p.vt + VtIndex(gv, d, m0 + 16 * b16 + (half ? 4 : 0),
+                                                   p.ldvt)) = v;
+      }
+      AsmFence();
+    }
+  } else {
+    // Past the last column: nothing to store, but the meetings are the
+    // work-group's.
+    piece_ready(std::integral_constant<int, 0>{});
+    piece_ready(std::integral_constant<int, 1>{});
+    piece_ready(std::integral_constant<int, 2>{});
+    piece_ready(std::integral_constant<int, 3>{});
+  }
+}
+
 template <Epilogue EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void PackedBigKernel(GemmParams p, int tiles_m, int k_steps) {
@@ -1033,9 +1253,13 @@ void PackedBigKernel(GemmParams p, int tiles_m, int k_steps) {
   WaitLoads<0>();
   __syncthreads();
 
-  // Each wave's head staged in its own quarter of the ring.
-  WaveEpilogue<XB, WB, EPI>(p, acc, m0 + 128 * wr, split, tile_n * 8 + 4 * wc, wave, lane, lds,
-                            wave * kHeadStage<XB>);
+  if constexpr (EPI == Epilogue::kQkvRope) {
+    BigQkvEpilogue(p, acc, m0, wr, tile_n * 8 + 4 * wc, wave, lane, lds);
+  } else {
+    // Each wave's head staged in its own quarter of the ring.
+    WaveEpilogue<XB, WB, EPI>(p, acc, m0 + 128 * wr, split, tile_n * 8 + 4 * wc, wave, lane, lds,
+                              wave * kHeadStage<XB>);
+  }
 }
 
 // Packs row-major W [rows][K] into the fragment order above: half8
@@ -1139,8 +1363,9 @@ void LaunchPackedBig(const GemmParams& p, const PackedPlan& plan, hipStream_t st
   Require((static_cast<size_t>(p.m) * p.lda + p.k) * 2 < (size_t{1} << 31) &&
               static_cast<size_t>(p.k / 64) * 2 * 4096 < (size_t{1} << 31),
           "gemm: operands too large for the 256 x 256 tile");
-  Dispatch(PackedBigKernel<EPI>, dim3(groups), dim3(256), kBigLds, stream, true, true, p,
-           tiles_m, p.k / 64);
+  Dispatch(PackedBigKernel<EPI>, dim3(groups), dim3(256),
+           EPI == Epilogue::kQkvRope ? kBigQkvLds : kBigLds, stream, true, true, p, tiles_m,
+           p.k / 64);
 }
 
 template <Epilogue EPI>

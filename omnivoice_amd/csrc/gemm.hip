@@ -554,14 +554,16 @@ int BandFor(int m, int k, int bm, int splits) {
 
 // Split count of the partial-slice GEMMs (o and down): a function of K
 // alone, so that a row's slices, and the order in which the row kernel sums
-// them, are the same whatever else is packed in the batch. Four slices where
-// each keeps at least two K steps (the released o and down: 8 and 12 steps
-// per slice), else three or two.
-// Two splits (K = 2048 and 3072: 16 and 24 K steps each): four halved the
-// K loop of each work-group but doubled the fp32 slices the next add + norm
-// reads back; with two, 10 s 555 -> 570, clone 332 -> 367 and four batched
-// chunks 608 -> 649 unmask steps/s (same box). Small M keeps its
-// parallelism with two-wave tiles (PlanPacked).
+// them, are the same whatever else is packed in the batch. Two splits where
+// each keeps at least two K steps (the released o and down: 16 and 24 K
+// steps each), else one. Four halved the K loop of each work-group but
+// doubled the fp32 slices the next add + norm reads back; with two, 10 s
+// 555 -> 570, clone 332 -> 367 and four batched chunks 608 -> 649 unmask
+// steps/s (same box). Three for down (16 K steps each) helped the short
+// utterances (10 s 573-578 -> 579-588, 2 s 876-878 -> 897) but not the long
+// ones, whose tiles then spill into a second round (clone 366 -> 347,
+// chunks 661 -> 634; same box). Small M keeps its parallelism with two-wave
+// tiles (PlanPacked).
 int PartialSplits(int k_steps) {
   return k_steps % 2 == 0 && k_steps / 2 >= 2 ? 2 : 1;
 }

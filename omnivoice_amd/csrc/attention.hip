@@ -727,7 +727,9 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
 // all; the two heads then run on separately from the softmax on, as in the
 // kernel above.
 template <int MAXR>
-constexpr int kSharedKeyBytes = kRound * MAXR * kQBytes;
+constexpr int kKeySlots = MAXR <= 4 ? MAXR : 3;  // key rounds resident in LDS
+template <int MAXR>
+constexpr int kSharedKeyBytes = kRound * kKeySlots<MAXR> * kQBytes;
 template <int MAXR>
 constexpr int kSharedFront = kSharedKeyBytes<MAXR> + 2 * kQBytes > kExactMerge<2>
                                  ? kSharedKeyBytes<MAXR> + 2 * kQBytes
@@ -741,7 +743,8 @@ constexpr int SharedKeyLds() {
 template <int MAXR>
 __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams p) {
   constexpr int GROUP = 2;
-  static_assert(MAXR >= 1 && MAXR <= 4, "shared-key kernel: 1 to 4 key tiles per wave");
+  static_assert(MAXR >= 1 && MAXR <= 6, "shared-key kernel: 1 to 6 key tiles per wave");
+  constexpr int kRing = kKeySlots<MAXR>;
   if (static_cast<int>(blockIdx.x) >= p.work_count * p.kv_heads) {
     PrefetchWeights(p.prefetch, static_cast<int>(blockIdx.x) - p.work_count * p.kv_heads);
     return;
@@ -791,8 +794,8 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
   const unsigned char* k_base = reinterpret_cast<const unsigned char*>(
       p.qk + static_cast<size_t>(p.heads + g) * p.ld_qk + static_cast<size_t>(block0) * 2048);
   auto dma_round = [&](int r) {
-    const int slot = kRound * r + (wave >> 1);
-    const int t = min(slot, tiles - 1);
+    const int slot = kRound * (r % kRing) + (wave >> 1);
+    const int t = min(kRound * r + (wave >> 1), tiles - 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int blk = 4 * (wave & 1) + i;
@@ -806,7 +809,7 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
   WaitLoads<0>();
   RingBarrier();
 #pragma unroll
-  for (int r = 1; r < MAXR; ++r)
+  for (int r = 1; r < kRing; ++r)
     dma_round(r);
 
   // Operand offsets (bytes) inside a 32-row tile: K step kk of the key and
@@ -845,8 +848,13 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
     if constexpr (j > 0) {
       // Round j has landed once every wave's own DMAs of it have: only the
       // later rounds' DMAs may still be in flight.
-      WaitLoads<4 * (MAXR - 1 - j)>();
+      constexpr int later = MAXR - 1 - j < kRing - 2 ? MAXR - 1 - j : kRing - 2;
+      WaitLoads<4 * later>();
       RingBarrier();
+      // Past the barrier no wave reads round j - 1 any more: its slot takes
+      // round j + kRing - 1 (five or six tiles per wave, three slots).
+      if constexpr (j + kRing - 1 < MAXR && j + kRing - 1 >= kRing)
+        dma_round(j + kRing - 1);
     }
     if constexpr (j == MAXR - 1) {
       // The first value tiles once every key tile has landed, so that they
@@ -857,7 +865,7 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
         load_value(std::integral_constant<int, 1>{});
     }
     if (j < mine) {
-      const unsigned char* tile = lds + (kRound * j + quarter) * kQBytes;
+      const unsigned char* tile = lds + (kRound * (j % kRing) + quarter) * kQBytes;
       half8 kf[8];
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
@@ -1048,12 +1056,14 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
       Dispatch(kernel, grid, dim3(64 * waves), lds_bytes, stream, true, !online, e);
     };
     // The kernel instance holds exactly the largest per-wave tile count.
-    if (group == 2 && p.exact_rounds <= 4) {
+    if (group == 2) {
       switch (p.exact_rounds) {
         case 1: launch(SharedKeyAttentionKernel<1>, 8, SharedKeyLds<1>()); break;
         case 2: launch(SharedKeyAttentionKernel<2>, 8, SharedKeyLds<2>()); break;
         case 3: launch(SharedKeyAttentionKernel<3>, 8, SharedKeyLds<3>()); break;
-        default: launch(SharedKeyAttentionKernel<4>, 8, SharedKeyLds<4>()); break;
+        case 4: launch(SharedKeyAttentionKernel<4>, 8, SharedKeyLds<4>()); break;
+        case 5: launch(SharedKeyAttentionKernel<5>, 8, SharedKeyLds<5>()); break;
+        default: launch(SharedKeyAttentionKernel<6>, 8, SharedKeyLds<6>()); break;
       }
     } else {
     switch (group * 8 + p.exact_rounds) {

@@ -2,11 +2,13 @@
 // matrix cores: replaces State::Attention's two batched GEMMs, the
 // materialised [heads][L][L] scores, SoftmaxKernel and MergeHeadsKernel of
 // the reference (generator.cpp:122-172, kernels/generator_kernels.hip:
-// 161-189). Scores never leave registers. Two kernels; which one a query
-// takes depends on its own sequence's length only (PlanAttentionWork):
-//  * ExactAttentionKernel, sequences of at most 768 keys (every shape of
-//    the generator's workloads): the reference's exact softmax, operands
-//    straight from memory into registers; described at the kernel below.
+// 161-189). Scores never leave registers. Which kernel a query takes
+// depends on its own sequence's length only (PlanAttentionWork):
+//  * sequences of at most 768 keys (every shape of the generator's
+//    workloads): the reference's exact softmax, in SharedKeyAttentionKernel
+//    (two query heads per kv head; queries and keys shared through LDS) or
+//    ExactAttentionKernel (one; operands straight from memory into
+//    registers), both described below;
 //  * AttentionKernel, longer sequences: online softmax over LDS-staged
 //    tiles, described next.
 //
@@ -369,14 +371,14 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // rescaled while keys stream, and the key quarters' partial outputs merge
 // as a plain sum.
 //
-// One work-group per (32-query tile, kv head) with 4 x GROUP / HPW waves:
-// wave w takes key tiles q, q + 4, q + 8, ... (q = w % 4) for HPW of the
-// GROUP query heads of the kv head. Every K and V^T operand goes from
-// memory straight into registers (QkIndex and
-// VtIndex store each 32-row tile's operands as whole 256-byte runs; with
-// HPW = GROUP each operand byte is used by exactly one wave, with HPW = 1
-// the waves of one quarter load the same tiles), as do the query operands:
-// the LDS holds only the softmax statistics and the final merge. A wave's tiles stream through a ring of
+// Two instances of it. ExactAttentionKernel (one query head per kv head,
+// GROUP = HPW = 1): one work-group per (32-query tile, kv head) with four
+// waves, wave w taking key tiles q, q + 4, q + 8, ... (q = w % 4). Every K
+// and V^T operand goes from memory straight into registers (QkIndex and
+// VtIndex store each 32-row tile's operands as whole 256-byte runs), as do
+// the query operands: the LDS holds only the softmax statistics and the
+// final merge. (Written for HPW of GROUP heads per wave; two query heads
+// per kv head take the shared-key kernel below.) A wave's tiles stream through a ring of
 // operand buffers, one or two tiles ahead: its key tiles, then its value
 // tiles, so the first value tiles load while the softmax runs. Every load
 // is unconditional (a slot past the wave's last tile re-reads a tile of the
@@ -387,14 +389,6 @@ __global__ __launch_bounds__((4 * GROUP + 1) * 64) void AttentionKernel(
 // are then formed in place and kept as the fp16 MFMA operand. Scores of up
 // to MAXR tiles per wave live in registers (16 floats per lane, tile and
 // head), so MAXR = 6 covers 768 keys.
-//
-// The phases are bound by different units of the CU: the operand loads by
-// its 64 bytes per clock of load return, the softmax by the quarter-rate
-// exp2, the products by the matrix cores, the merge by LDS. With one head
-// per wave the two heads' waves share a SIMD pairwise and exchange nothing,
-// so they meet per head (HeadSync) rather than at work-group barriers: the
-// head whose operands arrive first runs its softmax and products while the
-// other's loads are still landing.
 constexpr int kExactKeys = 768;
 constexpr int kExactMaxTiles = 6;   // per wave: 4 x 6 x 32 = 768 keys
 
@@ -405,24 +399,17 @@ __device__ __forceinline__ void UnrollEach(F&& f, std::integer_sequence<int, J..
   (f(std::integral_constant<int, J>{}), ...);
 }
 
-// LDS of the exact kernel: the merge's O^T slices (three per wave), and the
-// softmax statistics, maxima then sums. Where the two heads of a group meet
-// separately (one head per wave, two or more key tiles per wave; with one
-// tile the phases are too short to gain from it: 6.00 vs 5.97 us at 70 + 50
-// keys, against 7.07 vs 7.45 at 250 and 8.42 vs 8.90 at 330 + 250), the
-// statistics sit after the merge area, followed by one arrival counter per
-// head and meeting point (HeadSync); otherwise they share its space.
+// LDS of the exact kernels: the merge's O^T slices (three per wave) and the
+// softmax statistics, maxima then sums (in the register-fed kernel they
+// share the space: the statistics are dead once every wave is past the
+// barrier before the merge).
 template <int GROUP>
 constexpr int kExactMerge = 4 * 3 * GROUP * 16 * 64 * 4;
 template <int GROUP>
 constexpr int kExactStats = 2 * GROUP * kRound * 32 * 4;
 constexpr int kMeetings = 3;  // maxima, sums, merge
-template <int GROUP, int HPW, int MAXR>
-constexpr bool kHeadGroups = GROUP / HPW == 2 && MAXR >= 2;
-template <int GROUP, int HPW, int MAXR>
+template <int GROUP>
 constexpr int ExactLds() {
-  if constexpr (kHeadGroups<GROUP, HPW, MAXR>)
-    return kExactMerge<GROUP> + kExactStats<GROUP> + GROUP * kMeetings * 4;
   return kExactStats<GROUP> > kExactMerge<GROUP> ? kExactStats<GROUP> : kExactMerge<GROUP>;
 }
 
@@ -513,21 +500,6 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
   load_slot(std::integral_constant<int, 0>{});
   if constexpr (kDepth == 3)
     load_slot(std::integral_constant<int, 1>{});
-  constexpr bool kGroups = kHeadGroups<GROUP, HPW, MAXR>;
-  unsigned int* meet = reinterpret_cast<unsigned int*>(
-      lds + kExactMerge<GROUP> + kExactStats<GROUP>) + head0 * kMeetings;
-  if constexpr (kGroups) {
-    // Zero the counters before anyone arrives; the loads stay in flight.
-    if (threadIdx.x < GROUP * kMeetings)
-      reinterpret_cast<unsigned int*>(lds + kExactMerge<GROUP> + kExactStats<GROUP>)[threadIdx.x] = 0;
-    RingBarrier();
-  }
-  auto meet_head = [&](int point) {
-    if constexpr (kGroups)
-      HeadSync(meet + point);
-    else
-      RingBarrier();
-  };
 
   // Key phase: S^T = K Q^T per tile and head, unscaled; lane holds keys
   // 8 (e / 4) + 4 half_id + e % 4 of its query column. Keys past the
@@ -560,7 +532,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
   // Exact softmax over all keys: per-query maximum of the four quarters,
   // then the sum of e = exp2(c s - c max), c = log2(e) / sqrt(128) (c > 0,
   // so the maximum of the unscaled scores serves), then p = fp16(e / sum).
-  float* smax = reinterpret_cast<float*>(lds + (kGroups ? kExactMerge<GROUP> : 0));
+  float* smax = reinterpret_cast<float*>(lds);
   float* ssum = smax + GROUP * kRound * 32;
   float inverse[HPW];
   {
@@ -578,7 +550,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
       if (half_id == 0)
         smax[((head0 + h) * kRound + quarter) * 32 + col] = m[h];
     }
-    meet_head(0);
+    RingBarrier();
     float sum[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
@@ -597,7 +569,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
       if (half_id == 0)
         ssum[((head0 + h) * kRound + quarter) * 32 + col] = sum[h];
     }
-    meet_head(1);
+    RingBarrier();
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
       const float* hs = ssum + (head0 + h) * kRound * 32 + col;
@@ -645,11 +617,10 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
 
   // The four quarters' outputs are summed as ((0 + 1) + (2 + 3)); wave q
   // finishes dims 32 q .. + 31 of every head, its own part straight from
-  // registers. Where the statistics share the merge's space, they are dead
-  // once every wave is past a barrier.
+  // registers. The statistics are dead once every wave is past the
+  // barrier, so the merge reuses their space.
   floatx4* accs = reinterpret_cast<floatx4*>(lds);
-  if constexpr (!kGroups)
-    RingBarrier();
+  RingBarrier();
 #pragma unroll
   for (int h = 0; h < HPW; ++h)
 #pragma unroll
@@ -663,7 +634,7 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
             floatx4{o[h][dt][4 * k], o[h][dt][4 * k + 1], o[h][dt][4 * k + 2],
                     o[h][dt][4 * k + 3]};
     }
-  meet_head(2);
+  RingBarrier();
   if (col >= work.q_count)
     return;
 #pragma unroll
@@ -724,8 +695,18 @@ __global__ __launch_bounds__(256 * GROUP / HPW) void ExactAttentionKernel(Attent
 //
 // The DMAs of a key round (4 tiles, 32 KB) are spread over the eight waves,
 // and a work-group barrier after each round makes its tiles readable to
-// all; the two heads then run on separately from the softmax on, as in the
-// kernel above.
+// all. With five or six tiles per wave the key rounds pass through a ring
+// of three slots (96 KB), round r + 2 landing in round r - 1's slot once
+// every wave is past round r's barrier.
+//
+// The phases are bound by different units of the CU: the operand loads by
+// its 64 bytes per clock of load return, the softmax by the quarter-rate
+// exp2, the products by the matrix cores, the merge by LDS. The two heads'
+// waves share a SIMD pairwise and exchange nothing after the key phase, so
+// from the softmax on they meet per head (HeadSync) rather than at
+// work-group barriers: one head's softmax and products overlap the other's
+// (in the register-fed form of this kernel, 330 + 250 keys: 8.90 -> 8.42
+// us).
 template <int MAXR>
 constexpr int kKeySlots = MAXR <= 4 ? MAXR : 3;  // key rounds resident in LDS
 template <int MAXR>
@@ -1045,13 +1026,9 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
     AttentionParams e = p;
     e.work_count = p.exact_count;
     const dim3 grid(e.work_count * e.kv_heads + e.prefetch.groups);
-    // Up to four tiles per wave: two waves per SIMD, one query head each,
-    // so that one wave's softmax overlaps the other's MFMAs and loads (the
-    // two heads' waves of a quarter load the same operands, close enough
-    // in time to meet in L1); with five or six, one wave per SIMD doing
-    // both heads of the group, whose registers fit the longer score block
-    // (10 s: 8.5 vs 9.1 us, 2 s: 8.8 vs 9.0, clone: 20.7 vs 20.0, same
-    // box). A query's arithmetic is the same either way.
+    // Two query heads per kv head: the shared-key kernel (eight waves);
+    // one: the register-fed kernel (four waves). A query's arithmetic is
+    // the same either way.
     auto launch = [&](auto kernel, int waves, int lds_bytes) {
       Dispatch(kernel, grid, dim3(64 * waves), lds_bytes, stream, true, !online, e);
     };
@@ -1066,20 +1043,14 @@ void LaunchAttention(const AttentionParams& p, hipStream_t stream) {
         default: launch(SharedKeyAttentionKernel<6>, 8, SharedKeyLds<6>()); break;
       }
     } else {
-    switch (group * 8 + p.exact_rounds) {
-      case 9: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1, 1, 1>()); break;
-      case 10: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1, 1, 2>()); break;
-      case 11: launch(ExactAttentionKernel<1, 3, 1>, 4, ExactLds<1, 1, 3>()); break;
-      case 12: launch(ExactAttentionKernel<1, 4, 1>, 4, ExactLds<1, 1, 4>()); break;
-      case 13: launch(ExactAttentionKernel<1, 5, 1>, 4, ExactLds<1, 1, 5>()); break;
-      case 14: launch(ExactAttentionKernel<1, 6, 1>, 4, ExactLds<1, 1, 6>()); break;
-      case 17: launch(ExactAttentionKernel<2, 1, 1>, 8, ExactLds<2, 1, 1>()); break;
-      case 18: launch(ExactAttentionKernel<2, 2, 1>, 8, ExactLds<2, 1, 2>()); break;
-      case 19: launch(ExactAttentionKernel<2, 3, 1>, 8, ExactLds<2, 1, 3>()); break;
-      case 20: launch(ExactAttentionKernel<2, 4, 1>, 8, ExactLds<2, 1, 4>()); break;
-      case 21: launch(ExactAttentionKernel<2, 5, 2>, 4, ExactLds<2, 2, 5>()); break;
-      default: launch(ExactAttentionKernel<2, 6, 2>, 4, ExactLds<2, 2, 6>()); break;
-    }
+      switch (p.exact_rounds) {
+        case 1: launch(ExactAttentionKernel<1, 1, 1>, 4, ExactLds<1>()); break;
+        case 2: launch(ExactAttentionKernel<1, 2, 1>, 4, ExactLds<1>()); break;
+        case 3: launch(ExactAttentionKernel<1, 3, 1>, 4, ExactLds<1>()); break;
+        case 4: launch(ExactAttentionKernel<1, 4, 1>, 4, ExactLds<1>()); break;
+        case 5: launch(ExactAttentionKernel<1, 5, 1>, 4, ExactLds<1>()); break;
+        default: launch(ExactAttentionKernel<1, 6, 1>, 4, ExactLds<1>()); break;
+      }
     }
   }
   if (online) {

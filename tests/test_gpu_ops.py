@@ -258,11 +258,10 @@ def test_attention_head_groups_and_limits(heads, kv, seqs):
 @pytest.mark.parametrize("length", [100, 300, 500])
 def test_attention_batch_invariant(length):
     """A sequence's attention output does not depend on what else is packed
-    beside it: alone (one, three or four rounds of keys, taken by the kernel
-    that shares the keys through LDS) and packed after a 700-key sequence
-    (the register-fed kernel instance that holds six rounds) or a 1500-key
-    one (the online-softmax kernel for that one) it is bit for bit the
-    same."""
+    beside it: alone (the kernel instance for one, three or four rounds of
+    keys) and packed after a 700-key sequence (the instance that holds six
+    rounds, its keys passing through a three-slot ring) or a 1500-key one
+    (the online-softmax kernel for that one) it is bit for bit the same."""
     rng = np.random.default_rng(77 + length)
     heads, kv = 16, 8
     width = (heads + 2 * kv) * 128

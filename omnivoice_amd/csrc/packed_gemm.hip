@@ -105,6 +105,21 @@ __device__ __forceinline__ void Barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 }
 
+// Lanes l and l + 32 hold the two 8-byte halves of two 16-byte chunks, a
+// (their group 0) and b (group 1): lane l returns chunk a (a of lane l,
+// then a of lane l + 32), lane l + 32 chunk b (b of lane l, then b of lane
+// l + 32), by one v_permlane32_swap per dword.
+__device__ __forceinline__ half8 SwapHalves(half4 a, half4 b) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a);
+  const u32x2 ub = __builtin_bit_cast(u32x2, b);
+  const auto s0 = __builtin_amdgcn_permlane32_swap(ua[0], ub[0], false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(ua[1], ub[1], false, false);
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 out = {s0[0], s1[0], s0[1], s1[1]};
+  return __builtin_bit_cast(half8, out);
+}
+
 // Keeps the compiler from moving memory operations across this point.
 __device__ __forceinline__ void AsmFence() { asm volatile("" : : : "memory"); }
 
@@ -283,11 +298,15 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
     Barrier();  // LDS only: the rotary loads stay in flight
     if (qk && staged)
       load_rot(0, 0);
-    // q/k heads: normalised and rotated values go to this head's LDS
-    // staging rows (32 XB rows of 256 bytes at `stage`, 16-byte chunk c of
-    // row r at position c ^ (r % 16)), from which the waves that share the
-    // head store whole rows with 16-byte stores below (written straight
-    // from the MFMA layout, a store would cover 32 rows of 16 bytes each).
+    // q/k heads: lanes l and l + 32 hold the two 8-byte halves of each of
+    // two 16-byte chunks of a row (group g of lane half h: dims c_base + 8 g
+    // .. + 3 of the block, c_base = 16 (block % 4) + 4 h), so one swap of
+    // the upper and lower 32 lanes (v_permlane32_swap) gives lane half h the
+    // whole chunk of dims 16 (block % 4) + 8 h .. + 7, which it stores in the
+    // attention's operand order (QkIndex): a store covers 32 rows of 16
+    // bytes, two 256-byte runs per lane half. (Staged through LDS instead,
+    // to store 256-byte runs of 16 rows, it cost a second barrier and the
+    // LDS round trip.)
     if (qk) {
       const int first = WB == 2 ? (wave & ~1) : 0;  // the first wave of this head
       float scale[XB];
@@ -309,24 +328,26 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
         if (wb + 1 < WB)
           load_rope((wb + 1) & 1, wb + 1);
         const int f = wb & 1;
-        const int chunk0 = 2 * ((block0 + wb) & 3);  // chunks chunk0 + g, chunk0 + 8 + g
+        const int d0 = 16 * ((block0 + wb) & 3) + 8 * h;  // this lane's chunk after the swap
 #pragma unroll
         for (int b = 0; b < XB; ++b) {
-          const int r_local = 32 * b + col;
-          unsigned char* row = lds + stage + r_local * 256 + 8 * h;
+          half4 lo[2], hi[2];
 #pragma unroll
-          for (int g = 0; g < 2; ++g) {
-            half4 lo, hi;
+          for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const float2 cs = rot[f][b][4 * g + i];
               const float a = wt[f][4 * g + i] * (acc[wb][b][4 * g + i] * scale[b]);
               const float bb = wt[f][8 + 4 * g + i] * (acc[wb][b][4 * g + 8 + i] * scale[b]);
-              lo[i] = static_cast<half_t>(__builtin_fmaf(a, cs.x, -(bb * cs.y)));
-              hi[i] = static_cast<half_t>(__builtin_fmaf(bb, cs.x, a * cs.y));
+              lo[g][i] = static_cast<half_t>(__builtin_fmaf(a, cs.x, -(bb * cs.y)));
+              hi[g][i] = static_cast<half_t>(__builtin_fmaf(bb, cs.x, a * cs.y));
             }
-            *reinterpret_cast<half4*>(row + (((chunk0 + g) ^ (r_local & 15)) << 4)) = lo;
-            *reinterpret_cast<half4*>(row + (((chunk0 + 8 + g) ^ (r_local & 15)) << 4)) = hi;
+          const half8 lo_chunk = SwapHalves(lo[0], lo[1]);
+          const half8 hi_chunk = SwapHalves(hi[0], hi[1]);
+          const int m = m0 + 32 * b + col;
+          if (live && m < p.m) {
+            *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m, d0, p.ldq)) = lo_chunk;
+            *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m, 64 + d0, p.ldq)) = hi_chunk;
           }
         }
       }
@@ -350,24 +371,12 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
         }
       }
     }
-    Barrier();
+    // The value heads' staged V^T is read by the other waves of the head.
+    // Where one head fills the work-group (four waves per head), a q/k
+    // work-group has nothing staged and skips the barrier.
+    if (WB != 1 || !qk)
+      Barrier();
     if (qk) {
-      // The 4 / WB waves of this head copy its staged rows out in the
-      // attention's fragment order (QkIndex): 16 lanes store chunk q of 16
-      // consecutive rows, one 256-byte run.
-      constexpr int kLanes = 64 * (4 / WB);
-      const int t = (wave % (4 / WB)) * 64 + lane;
-#pragma unroll
-      for (int pass = 0; pass < 32 * XB * 16 / kLanes; ++pass) {
-        const int e = pass * kLanes + t;
-        const int r = (e & 15) + 16 * (e >> 8);
-        const int q = (e >> 4) & 15;
-        const int m = m0 + r;
-        const half8 v =
-            *reinterpret_cast<const half8*>(lds + stage + r * 256 + ((q ^ (r & 15)) << 4));
-        if (m < p.m)
-          *reinterpret_cast<half8*>(p.qk + QkIndex(slot, m, 8 * q, p.ldq)) = v;
-      }
     } else if (live && slot >= 0) {
       // The 4 / WB waves of this value head copy its staged V^T out in
       // 16-byte chunks (VtIndex): chunk (16-row block, dim group, half,

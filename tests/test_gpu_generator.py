@@ -300,6 +300,25 @@ def test_large_m_forward_matches_float32_oracle():
     gen.close()
 
 
+def test_released_dims_batch_matches_single_items():
+    """Released layer dimensions (2 layers): a batch that mixes a sequence
+    over 768 keys (the online-softmax attention) with short ones (the
+    shared-key attention, both launched for the one batch) gives every item
+    the codes and unmask order it gets alone."""
+    cfg = ov.released_config(layers=2)
+    gen = ov.Generator.synthetic(cfg, 77)
+    rng = np.random.default_rng(77)
+    shapes = [(20, 0, 50), (120, 0, 700), (9, 12, 45)]
+    items = [inp(random_input(rng, cfg, t, r, f), t, f) for t, r, f in shapes]
+    dec = ov.DecodingConfig()
+    results = gen.generate_batch(items, dec, seeds=[5, 6, 7])
+    for it, res, seed in zip(items, results, [5, 6, 7]):
+        single = gen.generate(it, dec, seed)
+        np.testing.assert_array_equal(single.codes, res.codes)
+        np.testing.assert_array_equal(single.unmasked_at, res.unmasked_at)
+    gen.close()
+
+
 @pytest.mark.parametrize("shape", [(80, 0, 250), (180, 125, 375)])
 def test_released_generate_properties(released, shape):
     cfg, gen, _ = released

@@ -154,6 +154,11 @@ struct PackedPlan {
   int splits = 1;  // K split (partial-slice epilogue only)
   int tiles = 0;   // row tiles x column tiles
   int nw = 4;      // waves (32-column blocks) of a 32 XB-row tile: 4, 2 or 1
+  // Column split (256 x 256 tiles only): the tile above covers columns
+  // [0, n_main) in whole rounds of work-groups, and a second launch covers
+  // [n_main, N) with the tail tile; 0 = one launch for every column.
+  int n_main = 0;
+  int tail_xb = 0, tail_wb = 0, tail_nw = 0, tail_tiles = 0;
 };
 PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue);
 void LaunchPacked(const GemmParams& p, const PackedPlan& plan, Epilogue epilogue,

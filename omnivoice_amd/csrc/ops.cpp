@@ -182,6 +182,7 @@ int ovg_op_linear_packed(const void* x, const void* w, float* y, int64_t rows,
     ovg::PackedPlan plan = ovg::PlanPacked(static_cast<int>(rows), static_cast<int>(out),
                                            static_cast<int>(in), epi);
     if (tile_rows != 0) {
+      plan.n_main = 0;  // one launch of the forced tile
       plan.xb = static_cast<int>(tile_rows / 32);
       plan.wb = tile_cols == 256 ? 2 : 1;
       plan.nw = tile_cols == 64 ? 2 : tile_cols == 32 ? 1 : 4;

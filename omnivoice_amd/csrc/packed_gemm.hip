@@ -1319,7 +1319,8 @@ __global__ void PackWeightsKernel(const T* w, const T* w2, int rows, int k,
 }
 
 template <int XB, Epilogue EPI, int NW>
-void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t stream, bool first,
+                    bool last) {
   const int tiles_m = (p.m + Packed<XB>::kBM - 1) / Packed<XB>::kBM;
   const int tiles_n = (p.n + 32 * NW - 1) / (32 * NW);
   const int groups = tiles_m * tiles_n * p.splits;
@@ -1328,42 +1329,45 @@ void LaunchPackedXB(const GemmParams& p, const PackedPlan& plan, hipStream_t str
     // The q/k/v tile stages its rotary rows when the grid is one round
     // (the kernel makes the same test on its grid size).
     const int lds = groups <= kCus ? NarrowLds<XB, EPI>() : Packed<XB>::kLds;
-    Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), lds, stream, true,
-             true, p, tiles_m, p.k / 64);
+    Dispatch(PackedGemmKernel<XB, EPI, NW>, dim3(groups), dim3(64 * NW), lds, stream, first,
+             last, p, tiles_m, p.k / 64);
     return;
   }
   // K ranges that are not a multiple of 256 per split (small models).
   Dispatch(PackedGemmKernel<XB, EPI, NW, true>, dim3(groups), dim3(64 * NW), Packed<XB>::kLds,
-           stream, true, true, p, tiles_m, p.k / 64);
+           stream, first, last, p, tiles_m, p.k / 64);
 }
 
 template <int XB, Epilogue EPI>
-void LaunchPackedNarrow(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+void LaunchPackedNarrow(const GemmParams& p, const PackedPlan& plan, hipStream_t stream,
+                        bool first, bool last) {
   if constexpr (EPI != Epilogue::kQkvRope) {
     if (plan.nw == 2) {
-      LaunchPackedXB<XB, EPI, 2>(p, plan, stream);
+      LaunchPackedXB<XB, EPI, 2>(p, plan, stream, first, last);
       return;
     }
     if (plan.nw == 1) {
-      LaunchPackedXB<XB, EPI, 1>(p, plan, stream);
+      LaunchPackedXB<XB, EPI, 1>(p, plan, stream, first, last);
       return;
     }
   }
-  LaunchPackedXB<XB, EPI, 4>(p, plan, stream);
+  LaunchPackedXB<XB, EPI, 4>(p, plan, stream, first, last);
 }
 
 template <Epilogue EPI>
-void LaunchPackedWide(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+void LaunchPackedWide(const GemmParams& p, const PackedPlan& plan, hipStream_t stream, bool first,
+                      bool last) {
   const int tiles_m = (p.m + 127) / 128;
   const int tiles_n = (p.n + 255) / 256;
   const int groups = tiles_m * tiles_n * p.splits;
   Require(groups == plan.tiles * plan.splits, "gemm: grid does not match the plan");
-  Dispatch(PackedWideKernel<EPI>, dim3(groups), dim3(256), kWideLds, stream, true, true, p,
+  Dispatch(PackedWideKernel<EPI>, dim3(groups), dim3(256), kWideLds, stream, first, last, p,
            tiles_m, p.k / 64);
 }
 
 template <Epilogue EPI>
-void LaunchPackedBig(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+void LaunchPackedBig(const GemmParams& p, const PackedPlan& plan, hipStream_t stream, bool first,
+                     bool last) {
   const int tiles_m = (p.m + 255) / 256;
   const int tiles_n = (p.n + 255) / 256;
   const int groups = tiles_m * tiles_n * p.splits;
@@ -1373,26 +1377,59 @@ void LaunchPackedBig(const GemmParams& p, const PackedPlan& plan, hipStream_t st
               static_cast<size_t>(p.k / 64) * 2 * 4096 < (size_t{1} << 31),
           "gemm: operands too large for the 256 x 256 tile");
   Dispatch(PackedBigKernel<EPI>, dim3(groups), dim3(256),
-           EPI == Epilogue::kQkvRope ? kBigQkvLds : kBigLds, stream, true, true, p, tiles_m,
+           EPI == Epilogue::kQkvRope ? kBigQkvLds : kBigLds, stream, first, last, p, tiles_m,
            p.k / 64);
 }
 
 template <Epilogue EPI>
-void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+void LaunchPackedShape(const GemmParams& p, const PackedPlan& plan, hipStream_t stream,
+                       bool first, bool last) {
   if (plan.xb == 8) {
-    LaunchPackedBig<EPI>(p, plan, stream);
+    LaunchPackedBig<EPI>(p, plan, stream, first, last);
     return;
   }
   if (plan.wb == 2) {
-    LaunchPackedWide<EPI>(p, plan, stream);
+    LaunchPackedWide<EPI>(p, plan, stream, first, last);
     return;
   }
   switch (plan.xb) {
-    case 1: LaunchPackedNarrow<1, EPI>(p, plan, stream); break;
-    case 2: LaunchPackedNarrow<2, EPI>(p, plan, stream); break;
-    case 3: LaunchPackedNarrow<3, EPI>(p, plan, stream); break;
-    default: LaunchPackedNarrow<4, EPI>(p, plan, stream); break;
+    case 1: LaunchPackedNarrow<1, EPI>(p, plan, stream, first, last); break;
+    case 2: LaunchPackedNarrow<2, EPI>(p, plan, stream, first, last); break;
+    case 3: LaunchPackedNarrow<3, EPI>(p, plan, stream, first, last); break;
+    default: LaunchPackedNarrow<4, EPI>(p, plan, stream, first, last); break;
   }
+}
+
+// One launch, or with a column split (PackedPlan::n_main) the main tile's
+// launch on columns [0, n_main) and the tail tile's on the rest: W from
+// packed block n_main / 32 on, outputs from column n_main (SwiGLU: act
+// column n_main / 2). Every tile sums the whole K range in the same order,
+// so a value does not depend on which launch computed it.
+template <Epilogue EPI>
+void LaunchPackedEpi(const GemmParams& p, const PackedPlan& plan, hipStream_t stream) {
+  if (plan.n_main == 0) {
+    LaunchPackedShape<EPI>(p, plan, stream, true, true);
+    return;
+  }
+  Require(plan.splits == 1 && EPI != Epilogue::kQkvRope && EPI != Epilogue::kPartial &&
+              plan.n_main % 256 == 0 && plan.n_main < p.n,
+          "gemm: column split only for unsplit store, accumulate and SwiGLU epilogues");
+  GemmParams head = p;
+  head.n = plan.n_main;
+  LaunchPackedShape<EPI>(head, plan, stream, true, false);
+  GemmParams tail = p;
+  tail.n = p.n - plan.n_main;
+  tail.w = p.w + static_cast<std::size_t>(plan.n_main) * p.k;
+  if constexpr (EPI == Epilogue::kSwiGlu)
+    tail.act = p.act + plan.n_main / 2;
+  else
+    tail.y = p.y + plan.n_main;
+  PackedPlan t;
+  t.xb = plan.tail_xb;
+  t.wb = plan.tail_wb;
+  t.nw = plan.tail_nw;
+  t.tiles = plan.tail_tiles;
+  LaunchPackedShape<EPI>(tail, t, stream, false, true);
 }
 
 }  // namespace
@@ -1454,34 +1491,67 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   struct Shape {
     int xb, wb, nw;
   };
-  double best = 0.0;
-  for (const Shape sh :
-       {Shape{8, 2, 4}, Shape{4, 2, 4}, Shape{4, 1, 4}, Shape{3, 1, 4}, Shape{2, 1, 4},
-        Shape{1, 1, 4}, Shape{4, 1, 2}, Shape{3, 1, 2}, Shape{2, 1, 2}, Shape{1, 1, 2},
-        Shape{2, 1, 1}, Shape{1, 1, 1}}) {
-    // The 256 x 256 tile's DMA offsets are 32-bit (X of the generator's
-    // GEMMs is [m][k]).
-    if (sh.xb == 8 && static_cast<size_t>(m) * k * 2 >= (size_t{1} << 31))
-      continue;
-    if (sh.nw < 4 && epilogue == Epilogue::kQkvRope)
-      continue;
-    const int cols = 32 * sh.nw * sh.wb;
-    const int tiles = (m + 32 * sh.xb - 1) / (32 * sh.xb) * ((n + cols - 1) / cols) * plan.splits;
-    const int full = tiles / kCus, rest = tiles % kCus;
-    const double rounds =
-        full == 0 ? 1.0
-                  : full + (rest == 0 ? 0.0 : std::max(0.5, static_cast<double>(rest) / kCus));
-    const double l2 = (32.0 * sh.xb + cols) * 128.0 / 64.0;
-    const double lds = (1.0 + sh.nw) * 32.0 * sh.xb * 128.0 / 128.0;
-    const double mfma = 4.0 * sh.xb * sh.wb * 32.0;
-    const double step = sh.xb == 8 ? 1500.0 : std::max(l2, std::max(lds, mfma));
-    const double cost = rounds * (static_cast<double>(steps) * step + 3200.0);
-    if (best == 0.0 || cost < best) {
-      best = cost;
-      plan.xb = sh.xb;
-      plan.wb = sh.wb;
-      plan.nw = sh.nw;
-      plan.tiles = tiles / plan.splits;
+  // The cheapest shape for n columns (the 256 x 256 tile only if `big`).
+  auto search = [&](int cols_n, bool big, PackedPlan* out) {
+    double best = 0.0;
+    for (const Shape sh :
+         {Shape{8, 2, 4}, Shape{4, 2, 4}, Shape{4, 1, 4}, Shape{3, 1, 4}, Shape{2, 1, 4},
+          Shape{1, 1, 4}, Shape{4, 1, 2}, Shape{3, 1, 2}, Shape{2, 1, 2}, Shape{1, 1, 2},
+          Shape{2, 1, 1}, Shape{1, 1, 1}}) {
+      // The 256 x 256 tile's DMA offsets are 32-bit (X of the generator's
+      // GEMMs is [m][k]).
+      if (sh.xb == 8 && (!big || static_cast<size_t>(m) * k * 2 >= (size_t{1} << 31)))
+        continue;
+      if (sh.nw < 4 && epilogue == Epilogue::kQkvRope)
+        continue;
+      const int cols = 32 * sh.nw * sh.wb;
+      const int tiles =
+          (m + 32 * sh.xb - 1) / (32 * sh.xb) * ((cols_n + cols - 1) / cols) * plan.splits;
+      const int full = tiles / kCus, rest = tiles % kCus;
+      const double rounds =
+          full == 0 ? 1.0
+                    : full + (rest == 0 ? 0.0 : std::max(0.5, static_cast<double>(rest) / kCus));
+      const double l2 = (32.0 * sh.xb + cols) * 128.0 / 64.0;
+      const double lds = (1.0 + sh.nw) * 32.0 * sh.xb * 128.0 / 128.0;
+      const double mfma = 4.0 * sh.xb * sh.wb * 32.0;
+      const double step = sh.xb == 8 ? 1500.0 : std::max(l2, std::max(lds, mfma));
+      const double cost = rounds * (static_cast<double>(steps) * step + 3200.0);
+      if (best == 0.0 || cost < best) {
+        best = cost;
+        out->xb = sh.xb;
+        out->wb = sh.wb;
+        out->nw = sh.nw;
+        out->tiles = tiles / plan.splits;
+      }
+    }
+  };
+  search(n, true, &plan);
+  // A 256 x 256 grid of between one and two rounds whose second round is
+  // at most half full runs those few work-groups at nearly a whole tile's
+  // time while the other CUs idle (gate/up at 3440 rows: 336 work-groups,
+  // 54 us against 37 for the one-round q/k/v of the same K). Where the
+  // epilogue allows a column offset, the tile then covers one round of
+  // column tiles and a second launch the remaining columns with the
+  // cheapest smaller tile (gate/up 54.0 -> 51.1 us; a 128 x 256 tail 52.1).
+  // With a fuller second round the second launch costs more than it saves
+  // (the audio heads at 3000 x 8200, 396 work-groups: 77 -> 84.5 us).
+  if (plan.xb == 8 && plan.splits == 1 &&
+      (epilogue == Epilogue::kStore || epilogue == Epilogue::kAccumulate ||
+       epilogue == Epilogue::kSwiGlu)) {
+    const int tiles_m = (m + 255) / 256;
+    const int tiles_n = (n + 255) / 256;
+    const int full = plan.tiles / kCus;
+    const int main_n = full * kCus / tiles_m;
+    const int rest = plan.tiles % kCus;
+    if (full == 1 && rest != 0 && 2 * rest <= kCus && main_n >= 1 && main_n < tiles_n) {
+      PackedPlan tail;
+      search(n - 256 * main_n, false, &tail);
+      plan.n_main = 256 * main_n;
+      plan.tiles = tiles_m * main_n;
+      plan.tail_xb = tail.xb;
+      plan.tail_wb = tail.wb;
+      plan.tail_nw = tail.nw;
+      plan.tail_tiles = tail.tiles;
     }
   }
   return plan;

@@ -129,12 +129,15 @@ def test_linear_matches_float64(rows, k, n, acc):
     (120, 1024, 4096, False), (580, 2048, 1024, True), (33, 512, 256, False),
     (500, 1024, 8200, False), (96, 384, 256, True), (1, 256, 128, False),
     (3440, 1024, 6144, False), (85, 256, 1024, False), (300, 64, 384, True),
-    (700, 704, 768, False)])
+    (700, 704, 768, False), (2048, 256, 8200, True)])
 def test_packed_linear_matches_float64_at_every_tile(rows, k, n, acc):
     """The generator's packed-weight kernel against float64, at every tile
     shape, and bit-identical across shapes (a row's result does not depend
     on the tile the packed row count selects). K = 64 and 704 leave the
-    256 x 256 tile's half-step ring a remainder of two."""
+    256 x 256 tile's half-step ring a remainder of two. At 3440 x 6144 and
+    2048 x 8200 the planned 256 x 256 grid would end in a partial round: the
+    plan splits the columns (6144 = 4608 + a 1536-column tail, 8200 = 8192 +
+    8), two launches whose results are the same bits as one."""
     rng = np.random.default_rng(rows + n + 7)
     x = rng.standard_normal((rows, k)).astype(np.float16)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)

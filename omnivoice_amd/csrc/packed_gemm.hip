@@ -1534,7 +1534,10 @@ PackedPlan PlanPacked(int m, int n, int k, Epilogue epilogue) {
   // column tiles and a second launch the remaining columns with the
   // cheapest smaller tile (gate/up 54.0 -> 51.1 us; a 128 x 256 tail 52.1).
   // With a fuller second round the second launch costs more than it saves
-  // (the audio heads at 3000 x 8200, 396 work-groups: 77 -> 84.5 us).
+  // (the audio heads at 3000 x 8200, 396 work-groups: 77 -> 84.5 us). The
+  // smaller tiles fit two work-groups per CU, so their grids of up to two
+  // rounds run at once (q/k/v at 1072 rows, 384 work-groups of 96 x 128:
+  // 19.1 us, against 24.3 split as 252 + 187 work-groups).
   if (plan.xb == 8 && plan.splits == 1 &&
       (epilogue == Epilogue::kStore || epilogue == Epilogue::kAccumulate ||
        epilogue == Epilogue::kSwiGlu)) {

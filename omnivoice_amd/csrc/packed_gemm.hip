@@ -376,8 +376,7 @@ __device__ __forceinline__ void WaveEpilogue(const GemmParams& p, floatx16 (&acc
     // work-group has nothing staged and skips the barrier.
     if (WB != 1 || !qk)
       Barrier();
-    if (qk) {
-    } else if (live && slot >= 0) {
+    if (!qk && live && slot >= 0) {
       // The 4 / WB waves of this value head copy its staged V^T out in
       // 16-byte chunks (VtIndex): chunk (16-row block, dim group, half,
       // dim 32) holds 8 keys of one dim; 32 lanes store 512 consecutive

@@ -197,10 +197,14 @@ struct WeightPrefetch {
   int groups;
 };
 
-// The prefetch work-group `group` (0 .. w.groups - 1): each thread keeps
-// eight 16-byte loads in flight (clamped in bounds, no load under a
-// condition) and folds them into a value that only an empty asm statement
-// consumes, so only the cache fill remains.
+// The prefetch work-group `group` (0 .. w.groups - 1): each thread issues
+// its 16-byte loads in batches of eight (clamped in bounds, no load under a
+// condition) and folds each batch into a value that only an empty asm
+// statement consumes, so only the cache fill remains. The next batch is
+// issued before the previous one is folded, so that eight to sixteen loads
+// stay in flight instead of the pipeline draining after every batch (2 s:
+// the attention launch carrying the 31.5 MB 8.06 -> 7.4-7.7 us, +0.5-0.8 %
+// unmask steps/s; batches of four or twelve no better).
 __device__ __forceinline__ void PrefetchWeights(const WeightPrefetch& w, int group) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   constexpr int kInFlight = 8;
@@ -211,16 +215,28 @@ __device__ __forceinline__ void PrefetchWeights(const WeightPrefetch& w, int gro
     if (chunks == 0)
       continue;
     const u32x4* src = reinterpret_cast<const u32x4*>(w.range[r]);
-    for (unsigned long long c = static_cast<unsigned long long>(group) * blockDim.x + threadIdx.x;
-         c < chunks; c += kInFlight * stride) {
-      u32x4 v[kInFlight];
+    unsigned long long c = static_cast<unsigned long long>(group) * blockDim.x + threadIdx.x;
+    if (c >= chunks)
+      continue;
+    u32x4 v[kInFlight];
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k)
+      v[k] = src[min(c + k * stride, chunks - 1)];
+    for (c += kInFlight * stride; c < chunks; c += kInFlight * stride) {
+      u32x4 next[kInFlight];
 #pragma unroll
       for (int k = 0; k < kInFlight; ++k)
-        v[k] = src[min(c + k * stride, chunks - 1)];
+        next[k] = src[min(c + k * stride, chunks - 1)];
 #pragma unroll
       for (int k = 0; k < kInFlight; ++k)
         fold ^= v[k].x;
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        v[k] = next[k];
     }
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k)
+      fold ^= v[k].x;
   }
   asm volatile("" : : "v"(fold));
 }

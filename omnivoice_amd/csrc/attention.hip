@@ -754,9 +754,11 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
   // Queries and keys into LDS by wave-wide DMAs of 1 KB, in key rounds:
   // wave w brings query blocks 2 w and 2 w + 1 (query tile b / 8 of the
   // group's heads), then in every round r blocks 4 (w % 2) .. + 3 of key
-  // tile 4 r + w / 2 (a tile past the sequence reloads its last tile into a
-  // slot that is never read), so every wave issues the same number of DMAs
-  // and the waits below are compile-time counts. The queries and round 0
+  // tile 4 r + w / 2 (a tile past the sequence in its last round reloads
+  // its last tile into a slot that is never read), so every wave issues the
+  // same DMAs, four per round, and a wait names the number of rounds still
+  // in flight. Rounds past the sequence's last (a shorter sequence in a
+  // launch sized for a longer one) are not loaded. The queries and round 0
   // land before the first barrier; the later rounds are issued after it
   // (issued together with round 0 they delay it: 8.4 against 8.26 us at
   // 330 + 250 keys) and land while the waves compute on the earlier ones.
@@ -784,6 +786,9 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
                lds0 + slot * kQBytes + blk * 1024);
     }
   };
+  // Rounds that hold keys of this sequence (the same for every wave); the
+  // instance's later rounds are neither loaded nor waited for here.
+  const int rounds = (tiles + kRound - 1) / kRound;
   dma_round(0);
   if (threadIdx.x < kSharedCounters)
     counters[threadIdx.x] = 0;
@@ -791,7 +796,8 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
   RingBarrier();
 #pragma unroll
   for (int r = 1; r < kRing; ++r)
-    dma_round(r);
+    if (r < rounds)
+      dma_round(r);
 
   // Operand offsets (bytes) inside a 32-row tile: K step kk of the key and
   // query operands; value-product operand f = 2 dt + j2 (halves, as above).
@@ -827,15 +833,26 @@ __global__ __launch_bounds__(512) void SharedKeyAttentionKernel(AttentionParams 
   auto key_tile = [&](auto jc) {
     constexpr int j = decltype(jc)::value;
     if constexpr (j > 0) {
-      // Round j has landed once every wave's own DMAs of it have: only the
-      // later rounds' DMAs may still be in flight.
-      constexpr int later = MAXR - 1 - j < kRing - 2 ? MAXR - 1 - j : kRing - 2;
-      WaitLoads<4 * later>();
-      RingBarrier();
-      // Past the barrier no wave reads round j - 1 any more: its slot takes
-      // round j + kRing - 1 (five or six tiles per wave, three slots).
-      if constexpr (j + kRing - 1 < MAXR && j + kRing - 1 >= kRing)
-        dma_round(j + kRing - 1);
+      if (j < rounds) {
+        // Round j has landed once every wave's own DMAs of it have: only
+        // the later rounds' DMAs may still be in flight, rounds j + 1 ..
+        // min(j + kRing - 2, rounds - 1), four per wave each.
+        constexpr int later = MAXR - 1 - j < kRing - 2 ? MAXR - 1 - j : kRing - 2;
+        const int pending = min(later, rounds - 1 - j);
+        if (later >= 2 && pending >= 2)
+          WaitLoads<8>();
+        else if (later >= 1 && pending >= 1)
+          WaitLoads<4>();
+        else
+          WaitLoads<0>();
+        RingBarrier();
+        // Past the barrier no wave reads round j - 1 any more: its slot
+        // takes round j + kRing - 1 (five or six tiles per wave, three
+        // slots).
+        if constexpr (j + kRing - 1 < MAXR && j + kRing - 1 >= kRing)
+          if (j + kRing - 1 < rounds)
+            dma_round(j + kRing - 1);
+      }
     }
     if constexpr (j == MAXR - 1) {
       // The first value tiles once every key tile has landed, so that they

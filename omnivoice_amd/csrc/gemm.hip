@@ -559,11 +559,13 @@ int BandFor(int m, int k, int bm, int splits) {
 // steps each), else one. Four halved the K loop of each work-group but
 // doubled the fp32 slices the next add + norm reads back; with two, 10 s
 // 555 -> 570, clone 332 -> 367 and four batched chunks 608 -> 649 unmask
-// steps/s (same box). Three for down (16 K steps each) helped the short
-// utterances (10 s 573-578 -> 579-588, 2 s 876-878 -> 897) but not the long
-// ones, whose tiles then spill into a second round (clone 366 -> 347,
-// chunks 661 -> 634; same box). Small M keeps its parallelism with two-wave
-// tiles (PlanPacked).
+// steps/s (same box). Three for down (16 K steps each) help the short
+// utterances and cost the long ones, re-measured on the current kernels:
+// 10 s 578-585 -> 587-595, 2 s 893 -> 915-917, clone 387 -> 377, four
+// chunks 689 -> 658 (its down 28.7 -> 35.8 us as 256 x 256 tiles, 43.5 as
+// 128 x 256 in 1.3 rounds; same boxes). The count cannot follow M without
+// making a row's sum depend on the batch, so two stay. Small M keeps its
+// parallelism with two-wave tiles (PlanPacked).
 int PartialSplits(int k_steps) {
   return k_steps % 2 == 0 && k_steps / 2 >= 2 ? 2 : 1;
 }

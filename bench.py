@@ -68,7 +68,7 @@ def make_input(ov, text, reference, target, seed=42):
 def host_cpu():
     """(model name, logical CPUs this process may run on, threads to use):
     every CPU in the affinity mask, capped by OMP_NUM_THREADS where it is set
-    (a one-GPU box's share of the host, 16)."""
+    (on a host shared by several GPUs, typically one GPU's share of it)."""
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
